@@ -1,0 +1,275 @@
+#!/usr/bin/env python
+"""Headline benchmark of the MI355X Soft-DTW engine (one JSON line on stdout).
+
+Workload: x, y ~ N(0,1) fp32, B=32, N=M=512, D=64, gamma=1,
+sqeuclidean; one step = SoftDTW(...)(x, y).sum().backward() with fresh leaf clones of the
+resident inputs, as in the reference's bench/bench_memory.py:51-58.  Both modes are timed:
+unfused (materialised (B,N,M) cost) and fused (cost recomputed per cell).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--mode both|unfused|fused]
+                    [--no-cpu-baseline] [--kernel NAME --launches L]
+
+`value` is unfused DP cells/s = B*N*M / (fwd+bwd seconds); the fused figures ride along in
+the same line.  `roofline` covers the dominant kernel (largest share of a step), timed with
+HIP events on the stream the engine launches on.  `cpu_baseline` times the CPU restatement
+of the reference's CPU path (oracle/) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sdtw-cuda-torch_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "fwd+bwd ms & DP cells/s at B=32 N=M=512 D=64 (unfused, fused); peak MB"
+HBM_PEAK_GBS = 8000.0
+# reference CSV artefact, bench/softdtw_memory_benchmark.csv:13 (unfused 20.102 ms)
+REF_UNFUSED_MS = 20.102
+REF_FUSED_MS = 141.358
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(B, N, M, K, seed=0):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, N, K, generator=g)
+    y = torch.randn(B, M, K, generator=g)
+    return x, y
+
+
+def algorithmic_bytes(kernel, B, N, M, K):
+    """Minimal HBM bytes one launch of `kernel` must move (fp32)."""
+    cells = B * N * M
+    xy = B * (N + M) * K
+    return {
+        "dist_fwd": 4 * (cells + xy),          # read x, y; write D
+        "dp_fwd": 4 * (2 * cells),             # read D; write R
+        "dp_bwd": 4 * (3 * cells),             # read D, R; write G
+        "dist_bwd": 4 * (cells + 2 * xy),      # read G, x, y; write gx, gy
+        "fused_fwd": 4 * (cells + xy),         # read x, y; write R
+        "fused_bwd_e": 4 * (2 * cells + xy),   # read R, x, y; write g*E
+    }[kernel]
+
+
+def kernel_launcher(name, xg, yg, gamma):
+    """Closure launching exactly one engine kernel family on torch's current stream."""
+    from softdtw_cuda import _engine
+
+    D = _engine.sqeuclid_fwd(xg, yg)
+    out, R = _engine.dtw_fwd(D, gamma, -1.0)
+    G = _engine.dtw_bwd(D, R, gamma, -1.0)
+    fn = {
+        "dist_fwd": lambda: _engine.sqeuclid_fwd(xg, yg),
+        "dp_fwd": lambda: _engine.dtw_fwd(D, gamma, -1.0),
+        "dp_bwd": lambda: _engine.dtw_bwd(D, R, gamma, -1.0),
+        "dist_bwd": lambda: _engine.sqeuclid_bwd(xg, yg, D, G, mask=True),
+        "fused_fwd": lambda: _engine.fused_fwd(xg, yg, gamma, -1.0),
+        "fused_bwd_e": lambda: _engine.fused_bwd_e(xg, yg, R, gamma, -1.0),
+    }[name]
+    return fn
+
+
+def time_kernel(fn, launches, warmup=2):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(launches)]
+    for a, b in evs:
+        a.record(st)
+        fn()
+        b.record(st)
+    torch.cuda.synchronize()
+    return statistics.mean(a.elapsed_time(b) for a, b in evs)
+
+
+def time_steps(step, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    st = torch.cuda.current_stream()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(st)
+    for _ in range(steps):
+        step()
+    b.record(st)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    peak = torch.cuda.max_memory_allocated() / 2 ** 20
+    return ms, peak
+
+
+def cpu_baseline(x, y, gamma, budget_s=15.0):
+    """The oracle (reference CPU path restated: torch-CPU distance + C DP + autograd),
+    fwd+bwd over the same headline batch, on this host's cores."""
+    import torch
+
+    import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, 16)  # the GPU box grants one GPU's share of host cores
+    torch.set_num_threads(cores)
+    oracle.load_library()
+
+    def run():
+        xo = x.clone().requires_grad_(True)
+        yo = y.clone().requires_grad_(True)
+        oracle.softdtw(xo, yo, gamma=gamma, nthreads=cores).sum().backward()
+
+    run()  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    B, N, K = x.shape
+    M = y.shape[1]
+    return {
+        "value": B * N * M / med,
+        "unit": "cells/s",
+        "cores": cores,
+        "kind": "port",
+        "ms_per_step": med * 1e3,
+        "sample": f"full headline batch B={B} N={N} M={M} D={K}, unfused CPU route "
+                  f"(torch-CPU distance + C/OpenMP DP over pairs), median of {len(times)} "
+                  f"fwd+bwd runs after 1 warm-up",
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--mode", choices=["both", "unfused", "fused"], default="both")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel", default=None,
+                    help="only launch one kernel family repeatedly (for rocprofv3 runs)")
+    ap.add_argument("--launches", type=int, default=20)
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this engine is measured on one GPU only (pairs shard across GPUs "
+              "with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from softdtw_cuda import SoftDTW
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+
+    B, N, M, K, gamma = 32, 512, 512, 64, 1.0
+    cells = B * N * M
+    x, y = make_inputs(B, N, M, K, seed=0)
+    X = x.cuda()
+    Y = y.cuda()
+
+    if args.kernel:
+        fn = kernel_launcher(args.kernel, X, Y, gamma)
+        ms = time_kernel(fn, args.launches)
+        log(f"kernel {args.kernel}: {ms:.4f} ms/launch over {args.launches} launches")
+        return 0
+
+    modes = ["unfused", "fused"] if args.mode == "both" else [args.mode]
+    res = {}
+    for mode in modes:
+        sdtw = SoftDTW(gamma=gamma, fused=(mode == "fused"))
+
+        def step():
+            xs = X.detach().clone().requires_grad_(True)
+            ys = Y.detach().clone().requires_grad_(True)
+            sdtw(xs, ys).sum().backward()
+
+        log(f"[bench] mode={mode} warmup={args.warmup} steps={args.steps}")
+        ms, peak = time_steps(step, args.steps, args.warmup)
+        res[mode] = {"ms_per_step": ms, "cells_per_s": cells / (ms * 1e-3), "peak_mib": peak}
+        log(f"[bench] mode={mode} {ms:.3f} ms/step  {cells / (ms * 1e-3):.3e} cells/s  peak {peak:.1f} MiB")
+
+    # per-kernel timing (HIP events on the engine's stream) -> dominant kernel roofline
+    kernels = []
+    if "unfused" in res:
+        kernels += ["dist_fwd", "dp_fwd", "dp_bwd", "dist_bwd"]
+    if "fused" in res:
+        kernels += ["fused_fwd", "fused_bwd_e"]
+    per = {}
+    for kname in kernels:
+        fn = kernel_launcher(kname, X, Y, gamma)
+        per[kname] = time_kernel(fn, max(5, min(args.steps, 20)))
+        log(f"[bench] kernel {kname}: {per[kname]:.4f} ms/launch")
+    dom = max(per, key=per.get)
+    abytes = algorithmic_bytes(dom, B, N, M, K)
+    achieved = abytes / (per[dom] * 1e-3) / 1e9
+    roofline = {
+        "bound": "hbm",
+        "kernel": dom,
+        "achieved": round(achieved, 3),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 6),
+        "traffic": None,
+        "algorithmic_bytes_per_launch": abytes,
+        "avg_launch_ms": round(per[dom], 5),
+        "diagonal_steps_per_launch": N + M - 1,
+        "ns_per_diagonal_step": round(per[dom] * 1e6 / (N + M - 1), 2),
+        "kernel_ms": {k: round(v, 5) for k, v in per.items()},
+    }
+
+    head = res.get("unfused") or res["fused"]
+    line = {
+        "metric": METRIC,
+        "value": head["cells_per_s"],
+        "unit": "cells/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": (head["cells_per_s"] / (cells / (REF_UNFUSED_MS * 1e-3)))
+        if "unfused" in res else None,
+        "dtype": "f32 (fp64 DP state)",
+        "data": "synthetic",
+        "config": {
+            "workload": "headline (BASELINE.json configs[1]): SoftDTW fwd+bwd, "
+                        "B=32 N=M=512 D=64 gamma=1 sqeuclidean, randn seed 0",
+            "B": B, "N": N, "M": M, "D": K, "gamma": gamma,
+            "value_mode": "unfused" if "unfused" in res else "fused",
+        },
+        "modes": {k: {kk: (round(vv, 4) if kk != "cells_per_s" else vv) for kk, vv in v.items()}
+                  for k, v in res.items()},
+        "reference_ms": {"unfused": REF_UNFUSED_MS, "fused": REF_FUSED_MS,
+                         "source": "bench/softdtw_memory_benchmark.csv:13 (unstated NVIDIA GPU)"},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline (oracle on host cores)")
+        line["cpu_baseline"] = cpu_baseline(x, y, gamma)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,128 @@
+/*
+ * sdtw.h -- C ABI of the MI355X (gfx950) Soft-DTW engine.
+ *
+ * The engine replaces the device-side operator boundary of BGU-CS-VIL/sdtw-cuda-torch:
+ * the six functions of softdtw_cuda/cuda/launcher.py that the autograd Functions call,
+ * plus the torch-op distance of softdtw_cuda/distances.py.  Every entry point below names
+ * the reference interface it stands in for.
+ *
+ * Conventions
+ *   - All tensor arguments are raw device pointers to contiguous row-major fp32 data.
+ *   - Shapes are int64: B pairs, N rows of x, M rows of y, K features.
+ *   - gamma > 0 and finite.  bandwidth <= 0 disables the Sakoe-Chiba band (the reference
+ *     maps None / <= 0 to -1.0, autograd.py:19-23); a positive band skips cells with
+ *     |i - j| > bandwidth exactly as the reference CPU path does (launcher.py:315,345).
+ *   - stream is a hipStream_t (torch's current stream); NULL is the null stream.  Every
+ *     call only enqueues work: nothing synchronises the device, nothing allocates or
+ *     frees device memory.  Scratch memory comes from the caller as `ws`/`ws_bytes`
+ *     (size it with sdtw_workspace_bytes).
+ *   - The return value is an sdtw_status; sdtw_strerror() describes it.
+ *   - R (the forward table kept for the backward) is engine-internal: fp32, (B, N, M)
+ *     unpadded, row-major, R[b,i,j] = the reference's R[b,i+1,j+1] (launcher.py:177) rounded
+ *     once from an fp64 recursion.  Out-of-band cells hold +inf.
+ *   - Re-entrant and stateless apart from a once-only device-attribute query.
+ */
+#ifndef SDTW_H_
+#define SDTW_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum sdtw_status {
+    SDTW_OK = 0,
+    SDTW_ERR_INVALID_VALUE = 1,  /* bad shape, gamma, pointer */
+    SDTW_ERR_WORKSPACE = 2,      /* ws too small (see sdtw_workspace_bytes) */
+    SDTW_ERR_LAUNCH = 3,         /* hipLaunchKernel / runtime error */
+    SDTW_ERR_UNSUPPORTED = 4     /* shape outside what the kernels support */
+} sdtw_status;
+
+/* Operation selectors for sdtw_workspace_bytes. */
+typedef enum sdtw_op {
+    SDTW_OP_SQEUCLID_FWD = 0,
+    SDTW_OP_SQEUCLID_BWD = 1,
+    SDTW_OP_FWD = 2,
+    SDTW_OP_BWD = 3,
+    SDTW_OP_FUSED_FWD = 4,
+    SDTW_OP_FUSED_BWD = 5
+} sdtw_op;
+
+/* Distance modes for sdtw_sqeuclid_fwd_f32. */
+typedef enum sdtw_dist_mode {
+    /* Same fp32 bits as the reference's torch-CPU distance (distances.py:20-28) on an x86
+     * host: row norms in ATen's 8-lane cascade order, x.y^T as a sequential FMA chain over
+     * k (plain multiply-then-add when K*N*M < 400, ATen's small-matrix kernel). */
+    SDTW_DIST_EXACT = 0,
+    /* x.y^T on the matrix cores (v_mfma_f32_16x16x4_f32); norms as in EXACT.  Faster, but
+     * the k-sum is reassociated, so D differs from the reference by a few ulp. */
+    SDTW_DIST_MFMA = 1
+} sdtw_dist_mode;
+
+const char *sdtw_strerror(int status);
+int sdtw_version(void);
+
+/* Bytes of caller-provided scratch that `op` needs at this shape (0 if none). */
+size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K);
+
+/* D[b,i,j] = max(0, (|x_bi|^2 + |y_bj|^2) - 2 x_bi . y_bj)  -> D (B,N,M).
+ * Replaces softdtw_cuda/distances.py:6-28 (sqeuclidean / pairwise_distance). */
+int sdtw_sqeuclid_fwd_f32(const float *x, const float *y, float *D, int64_t B, int64_t N,
+                          int64_t M, int64_t K, int mode, void *ws, size_t ws_bytes,
+                          void *stream);
+
+/* Gradient of the distance above given G = dL/dD (B,N,M):
+ *   G' = G where (x2 + y2 - 2xy) >= 0 else 0            (clamp_min backward)
+ *   gx = 2 (x * rowsum(G') - G' y),  gy = 2 (y * colsum(G') - G'^T x)
+ * D is the clamped forward output (used to find clamped cells).  mask = 0 skips the clamp
+ * mask (the fused-mode chain rule of autograd_xy.py:45-49 has none).
+ * Replaces the torch autograd backward of distances.py:20-28 (bmm/sum/clamp_min
+ * backward) and, with mask = 0, autograd_xy.py:41-49. */
+int sdtw_sqeuclid_bwd_f32(const float *x, const float *y, const float *D, const float *G,
+                          float *gx, float *gy, int64_t B, int64_t N, int64_t M, int64_t K,
+                          int mask, void *ws, size_t ws_bytes, void *stream);
+
+/* Soft-DTW forward over a materialised cost D (B,N,M): R (B,N,M) and out[b] = R[b,N-1,M-1].
+ * Replaces softdtw_cuda/cuda/launcher.py:167-223 (softdtw_forward_cuda) with the
+ * numerics of the reference CPU path launcher.py:307-324 (fp64 recursion, fp32 R). */
+int sdtw_fwd_f32(const float *D, float *R, float *out, int64_t B, int64_t N, int64_t M,
+                 double gamma, double bandwidth, void *ws, size_t ws_bytes, void *stream);
+
+/* Soft-DTW backward: G[b,i,j] = gout[b] * E[b,i,j], E = d out[b] / d D[b,i,j].
+ * gout may be NULL (treated as 1, i.e. G = E, what launcher.py returns).
+ * Replaces softdtw_cuda/cuda/launcher.py:226-300 (softdtw_backward_cuda_log) together
+ * with the `g * E` of autograd.py:46-47, with the numerics of launcher.py:327-353. */
+int sdtw_bwd_f32(const float *D, const float *R, const float *gout, float *G, int64_t B,
+                 int64_t N, int64_t M, double gamma, double bandwidth, void *ws,
+                 size_t ws_bytes, void *stream);
+
+/* Fused forward: cost recomputed per cell from x (B,N,K), y (B,M,K) with the same bits as
+ * sdtw_sqeuclid_fwd_f32(EXACT); no (B,N,M) cost tensor exists.
+ * Replaces softdtw_cuda/cuda/launcher.py:33-87 (softdtw_forward_cuda_fused_sqeuclid). */
+int sdtw_fused_fwd_f32(const float *x, const float *y, float *R, float *out, int64_t B,
+                       int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
+                       void *ws, size_t ws_bytes, void *stream);
+
+/* Fused backward: E recomputed with per-cell costs from x, y, then
+ *   gx = 2 (x * rowsum(gE) - gE y),  gy = 2 (y * colsum(gE) - gE^T x),  gE = gout[b] * E.
+ * gout may be NULL (treated as 1).  E lives only in the workspace.
+ * Replaces softdtw_cuda/cuda/launcher.py:90-162 (softdtw_backward_cuda_fused_sqeuclid)
+ * together with the chain rule of autograd_xy.py:32-51. */
+int sdtw_fused_bwd_f32(const float *x, const float *y, const float *R, const float *gout,
+                       float *gx, float *gy, int64_t B, int64_t N, int64_t M, int64_t K,
+                       double gamma, double bandwidth, void *ws, size_t ws_bytes,
+                       void *stream);
+
+/* Fused backward, E only: E (B,N,M) = d out / d D with per-cell costs from x, y.
+ * Replaces softdtw_cuda/cuda/launcher.py:90-162 exactly (it returns E). */
+int sdtw_fused_bwd_e_f32(const float *x, const float *y, const float *R, const float *gout,
+                         float *E, int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
+                         double bandwidth, void *ws, size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDTW_H_ */

@@ -1,0 +1,311 @@
+// sdtw_capi.hip -- the extern "C" boundary declared in include/sdtw.h.
+//
+// Responsibilities: argument validation, carving the caller's workspace, choosing kernel
+// variants and enqueueing them on the caller's stream.  No allocation, no synchronisation.
+#include <math.h>
+
+#include "../../include/sdtw.h"
+#include "sdtw_internal.hpp"
+
+using namespace sdtw;
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Sub-buffer carving of a caller workspace.
+struct Carver {
+    char* base;
+    size_t cap;
+    size_t off = 0;
+    bool ok = true;
+    template <class T>
+    T* take(size_t count) {
+        const size_t bytes = align_up(count * sizeof(T));
+        if (base == nullptr || off + bytes > cap) {
+            ok = false;
+            off += bytes;
+            return nullptr;
+        }
+        T* p = reinterpret_cast<T*>(base + off);
+        off += bytes;
+        return p;
+    }
+};
+
+bool shape_ok(int64_t B, int64_t N, int64_t M, int64_t K, bool need_k) {
+    if (B < 0 || N <= 0 || M <= 0) return false;
+    if (need_k && K <= 0) return false;
+    // kernels index with int; keep every dimension and per-pair table within range
+    if (B > INT32_MAX || N > INT32_MAX || M > INT32_MAX || K > INT32_MAX) return false;
+    if (N * M > (int64_t)INT32_MAX * 16) return false;
+    return true;
+}
+
+// distance kernels put B on grid.z and row tiles on grid.y (<= 65535 each)
+bool dist_grid_ok(int64_t B, int64_t N, int64_t M) {
+    return B <= 65535 && (N + 63) / 64 <= 65535 && (M + 63) / 64 <= 65535 &&
+           (N + 255) / 256 <= 65535 && (M + 255) / 256 <= 65535;
+}
+
+bool gamma_ok(double gamma) { return gamma > 0.0 && isfinite(gamma); }
+
+// ATen's naive bmm kernel (multiply, then add) runs when K*N*M < 400.
+bool small_bmm(int64_t N, int64_t M, int64_t K) { return K * N * M < 400; }
+
+size_t ws_norms(int64_t B, int64_t N, int64_t M) {
+    return align_up(sizeof(float) * B * N) + align_up(sizeof(float) * B * M);
+}
+
+int status_of(hipError_t e) { return e == hipSuccess ? SDTW_OK : SDTW_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+const char* sdtw_strerror(int status) {
+    switch (status) {
+        case SDTW_OK: return "success";
+        case SDTW_ERR_INVALID_VALUE: return "invalid argument (shape, gamma or pointer)";
+        case SDTW_ERR_WORKSPACE: return "workspace too small (see sdtw_workspace_bytes)";
+        case SDTW_ERR_LAUNCH: return "HIP kernel launch failed";
+        case SDTW_ERR_UNSUPPORTED: return "unsupported configuration";
+        default: return "unknown sdtw status";
+    }
+}
+
+int sdtw_version(void) { return 1; }
+
+size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) {
+    (void)K;
+    if (B < 0 || N < 0 || M < 0) return 0;
+    switch (op) {
+        case SDTW_OP_SQEUCLID_FWD:
+        case SDTW_OP_SQEUCLID_BWD:
+            return ws_norms(B, N, M);
+        case SDTW_OP_FWD:
+            return align_up(sizeof(double) * B * M);
+        case SDTW_OP_BWD:
+            return align_up(sizeof(float) * B * 3 * (M + 1));
+        case SDTW_OP_FUSED_FWD:
+            return ws_norms(B, N, M) + align_up(sizeof(double) * B * M);
+        case SDTW_OP_FUSED_BWD:
+            return ws_norms(B, N, M) + align_up(sizeof(float) * B * 3 * (M + 1)) +
+                   align_up(sizeof(float) * B * N * M);
+        default:
+            return 0;
+    }
+}
+
+int sdtw_sqeuclid_fwd_f32(const float* x, const float* y, float* D, int64_t B, int64_t N,
+                          int64_t M, int64_t K, int mode, void* ws, size_t ws_bytes,
+                          void* stream) {
+    if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!x || !y || !D) return SDTW_ERR_INVALID_VALUE;
+    if (mode != SDTW_DIST_EXACT) return SDTW_ERR_UNSUPPORTED;
+    if (!dist_grid_ok(B, N, M)) return SDTW_ERR_UNSUPPORTED;
+    Carver c{static_cast<char*>(ws), ws_bytes};
+    DistParams p{};
+    p.x = x;
+    p.y = y;
+    p.x2 = c.take<float>(B * N);
+    p.y2 = c.take<float>(B * M);
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    p.D = D;
+    p.B = (int)B;
+    p.N = (int)N;
+    p.M = (int)M;
+    p.K = (int)K;
+    return status_of(launch_dist(p, small_bmm(N, M, K), false, (hipStream_t)stream));
+}
+
+int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const float* G,
+                          float* gx, float* gy, int64_t B, int64_t N, int64_t M, int64_t K,
+                          int mask, void* ws, size_t ws_bytes, void* stream) {
+    if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!x || !y || !G || !gx || !gy || (mask && !D)) return SDTW_ERR_INVALID_VALUE;
+    if (!dist_grid_ok(B, N, M)) return SDTW_ERR_UNSUPPORTED;
+    hipStream_t st = (hipStream_t)stream;
+    DistBwdParams p{};
+    p.x = x;
+    p.y = y;
+    p.D = mask ? D : nullptr;
+    p.G = G;
+    p.gx = gx;
+    p.gy = gy;
+    p.B = (int)B;
+    p.N = (int)N;
+    p.M = (int)M;
+    p.K = (int)K;
+    p.mask = mask ? 1 : 0;
+    p.muladd = small_bmm(N, M, K) ? 1 : 0;
+    if (mask) {
+        Carver c{static_cast<char*>(ws), ws_bytes};
+        float* x2 = c.take<float>(B * N);
+        float* y2 = c.take<float>(B * M);
+        if (!c.ok) return SDTW_ERR_WORKSPACE;
+        hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
+        if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
+        if (e != hipSuccess) return SDTW_ERR_LAUNCH;
+        p.x2 = x2;
+        p.y2 = y2;
+    }
+    return status_of(launch_dist_bwd(p, st));
+}
+
+int sdtw_fwd_f32(const float* D, float* R, float* out, int64_t B, int64_t N, int64_t M,
+                 double gamma, double bandwidth, void* ws, size_t ws_bytes, void* stream) {
+    if (!shape_ok(B, N, M, 1, false) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!D || !R || !out) return SDTW_ERR_INVALID_VALUE;
+    Carver c{static_cast<char*>(ws), ws_bytes};
+    FwdParams p{};
+    p.D = D;
+    p.R = R;
+    p.out = out;
+    p.edge = c.take<double>(B * M);
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    p.B = (int)B;
+    p.N = (int)N;
+    p.M = (int)M;
+    p.K = 0;
+    p.gamma = gamma;
+    p.bw = bandwidth;
+    return status_of(launch_fwd(p, false, false, (hipStream_t)stream));
+}
+
+int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, int64_t B,
+                 int64_t N, int64_t M, double gamma, double bandwidth, void* ws,
+                 size_t ws_bytes, void* stream) {
+    if (!shape_ok(B, N, M, 1, false) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!D || !R || !G) return SDTW_ERR_INVALID_VALUE;
+    Carver c{static_cast<char*>(ws), ws_bytes};
+    BwdParams p{};
+    p.D = D;
+    p.R = R;
+    p.gout = gout;
+    p.G = G;
+    p.edge = c.take<float>(B * 3 * (M + 1));
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    p.B = (int)B;
+    p.N = (int)N;
+    p.M = (int)M;
+    p.K = 0;
+    p.gamma = gamma;
+    p.bw = bandwidth;
+    return status_of(launch_bwd(p, false, false, (hipStream_t)stream));
+}
+
+int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int64_t B,
+                       int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
+                       void* ws, size_t ws_bytes, void* stream) {
+    if (!shape_ok(B, N, M, K, true) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!x || !y || !R || !out) return SDTW_ERR_INVALID_VALUE;
+    hipStream_t st = (hipStream_t)stream;
+    Carver c{static_cast<char*>(ws), ws_bytes};
+    FwdParams p{};
+    float* x2 = c.take<float>(B * N);
+    float* y2 = c.take<float>(B * M);
+    p.edge = c.take<double>(B * M);
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
+    if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
+    if (e != hipSuccess) return SDTW_ERR_LAUNCH;
+    p.x = x;
+    p.y = y;
+    p.x2 = x2;
+    p.y2 = y2;
+    p.R = R;
+    p.out = out;
+    p.B = (int)B;
+    p.N = (int)N;
+    p.M = (int)M;
+    p.K = (int)K;
+    p.gamma = gamma;
+    p.bw = bandwidth;
+    return status_of(launch_fwd(p, true, small_bmm(N, M, K), st));
+}
+
+// Fused backward core: norms, then the reverse wavefront writing gout * E into `E`.
+// Workspace layout: [x2 (B*N)][y2 (B*M)][edge (B*3*(M+1))][E (B*N*M), fused grads only].
+static int fused_bwd_common(const float* x, const float* y, const float* R, const float* gout,
+                            float* E, float* x2, float* y2, float* edge, int64_t B, int64_t N,
+                            int64_t M, int64_t K, double gamma, double bandwidth,
+                            hipStream_t st) {
+    hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
+    if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
+    if (e != hipSuccess) return SDTW_ERR_LAUNCH;
+    BwdParams p{};
+    p.x = x;
+    p.y = y;
+    p.x2 = x2;
+    p.y2 = y2;
+    p.R = R;
+    p.gout = gout;
+    p.G = E;
+    p.edge = edge;
+    p.B = (int)B;
+    p.N = (int)N;
+    p.M = (int)M;
+    p.K = (int)K;
+    p.gamma = gamma;
+    p.bw = bandwidth;
+    return status_of(launch_bwd(p, true, small_bmm(N, M, K), st));
+}
+
+int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const float* gout,
+                       float* gx, float* gy, int64_t B, int64_t N, int64_t M, int64_t K,
+                       double gamma, double bandwidth, void* ws, size_t ws_bytes,
+                       void* stream) {
+    if (!shape_ok(B, N, M, K, true) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!x || !y || !R || !gx || !gy) return SDTW_ERR_INVALID_VALUE;
+    if (!dist_grid_ok(B, N, M)) return SDTW_ERR_UNSUPPORTED;
+    hipStream_t st = (hipStream_t)stream;
+    Carver c{static_cast<char*>(ws), ws_bytes};
+    float* x2 = c.take<float>(B * N);
+    float* y2 = c.take<float>(B * M);
+    float* edge = c.take<float>(B * 3 * (M + 1));
+    float* Ebuf = c.take<float>(B * N * M);
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    int rc = fused_bwd_common(x, y, R, gout, Ebuf, x2, y2, edge, B, N, M, K, gamma, bandwidth, st);
+    if (rc != SDTW_OK) return rc;
+    DistBwdParams q{};
+    q.x = x;
+    q.y = y;
+    q.x2 = x2;
+    q.y2 = y2;
+    q.D = nullptr;
+    q.G = Ebuf;
+    q.gx = gx;
+    q.gy = gy;
+    q.B = (int)B;
+    q.N = (int)N;
+    q.M = (int)M;
+    q.K = (int)K;
+    q.mask = 0;
+    q.muladd = small_bmm(N, M, K) ? 1 : 0;
+    return status_of(launch_dist_bwd(q, st));
+}
+
+int sdtw_fused_bwd_e_f32(const float* x, const float* y, const float* R, const float* gout,
+                         float* E, int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
+                         double bandwidth, void* ws, size_t ws_bytes, void* stream) {
+    if (!shape_ok(B, N, M, K, true) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!x || !y || !R || !E) return SDTW_ERR_INVALID_VALUE;
+    Carver c{static_cast<char*>(ws), ws_bytes};
+    float* x2 = c.take<float>(B * N);
+    float* y2 = c.take<float>(B * M);
+    float* edge = c.take<float>(B * 3 * (M + 1));
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    return fused_bwd_common(x, y, R, gout, E, x2, y2, edge, B, N, M, K, gamma, bandwidth,
+                            (hipStream_t)stream);
+}
+
+}  // extern "C"

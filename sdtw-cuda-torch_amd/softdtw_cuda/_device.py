@@ -1,0 +1,27 @@
+"""Where the engine computes, and how tensors get there.
+
+The engine has one implementation: HIP kernels on a ROCm GPU.  GPU tensors are used in
+place; CPU tensors are staged to the current GPU and results are returned on the caller's
+device (autograd follows the copies).  Without a visible GPU this raises: there is no CPU
+implementation behind the API.  Kernels compute in float32; other floating dtypes are
+converted on entry and results are returned in the caller's dtype.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def compute_device(t: torch.Tensor) -> torch.device:
+    if t.is_cuda:
+        return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError(
+            "softdtw_cuda: this engine computes on a ROCm GPU (MI355X/gfx950) and no GPU is "
+            "visible; CPU tensors are staged through the GPU, so they cannot be processed here."
+        )
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def to_engine(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """float32, contiguous, on `device` (a no-op view when already so)."""
+    return t.to(device=device, dtype=torch.float32).contiguous()

@@ -1,0 +1,257 @@
+"""ctypes binding of the gfx950 Soft-DTW engine (libsdtw_hip.so, C ABI in include/sdtw.h).
+
+Every function here takes CUDA (ROCm) fp32 contiguous tensors, allocates outputs and the
+workspace through torch's caching allocator, and enqueues the engine's kernels on torch's
+current stream.  There is no CPU implementation behind these functions: if the library is
+missing or no GPU is present, they raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libsdtw_hip.so")
+_lib = None
+_lock = threading.Lock()
+
+# include/sdtw.h enums
+OP_SQEUCLID_FWD, OP_SQEUCLID_BWD, OP_FWD, OP_BWD, OP_FUSED_FWD, OP_FUSED_BWD = range(6)
+DIST_EXACT, DIST_MFMA = 0, 1
+
+_SIGS = {
+    "sdtw_strerror": ([ctypes.c_int], ctypes.c_char_p),
+    "sdtw_version": ([], ctypes.c_int),
+    "sdtw_workspace_bytes": ([ctypes.c_int] + [ctypes.c_int64] * 4, ctypes.c_size_t),
+    "sdtw_sqeuclid_fwd_f32": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4
+                              + [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+                              ctypes.c_int),
+    "sdtw_sqeuclid_bwd_f32": ([ctypes.c_void_p] * 6 + [ctypes.c_int64] * 4
+                              + [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+                              ctypes.c_int),
+    "sdtw_fwd_f32": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3
+                     + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+                     ctypes.c_int),
+    "sdtw_bwd_f32": ([ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3
+                     + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+                     ctypes.c_int),
+    "sdtw_fused_fwd_f32": ([ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4
+                           + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+                           ctypes.c_int),
+    "sdtw_fused_bwd_f32": ([ctypes.c_void_p] * 6 + [ctypes.c_int64] * 4
+                           + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+                           ctypes.c_int),
+    "sdtw_fused_bwd_e_f32": ([ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4
+                             + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+                             ctypes.c_int),
+}
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def load():
+    """Load libsdtw_hip.so (once).  Raises RuntimeError if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"softdtw_cuda: HIP engine library not found at {_LIB_PATH}. "
+                "Build it with `python sdtw-cuda-torch_amd/build.py` (hipcc, gfx950)."
+            )
+        lib = ctypes.CDLL(_LIB_PATH)
+        for name, (args, res) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+        return lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def strerror(rc: int) -> str:
+    return load().sdtw_strerror(int(rc)).decode()
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        raise RuntimeError(f"softdtw_cuda: {what} failed: {strerror(rc)} (status {rc})")
+
+
+def require_gpu(t: torch.Tensor, what: str):
+    if not t.is_cuda:
+        raise RuntimeError(f"softdtw_cuda: {what} expects a ROCm/CUDA tensor, got {t.device}")
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise RuntimeError(f"softdtw_cuda: {what} expects contiguous float32, got {t.dtype}")
+
+
+def _check_shapes(x=None, y=None, D=None, R=None, gout=None):
+    """Validate every operand's shape against the others before any launch: the kernels
+    trust B, N, M, K."""
+    B = N = M = K = None
+    if x is not None:
+        if x.dim() != 3:
+            raise ValueError(f"softdtw_cuda: x must be (B,N,K), got {tuple(x.shape)}")
+        B, N, K = x.shape
+    if y is not None:
+        if y.dim() != 3 or (B is not None and (y.shape[0] != B or y.shape[2] != K)):
+            raise ValueError(f"softdtw_cuda: y must be (B,M,K) matching x, got {tuple(y.shape)}")
+        B, M, K = y.shape
+    for name, t in (("D", D), ("R", R)):
+        if t is None:
+            continue
+        if t.dim() != 3:
+            raise ValueError(f"softdtw_cuda: {name} must be (B,N,M), got {tuple(t.shape)}")
+        if B is None:
+            B, N, M = t.shape
+        elif tuple(t.shape) != (B, N, M):
+            raise ValueError(f"softdtw_cuda: {name} shape {tuple(t.shape)} != {(B, N, M)}")
+    if gout is not None and gout.numel() != B:
+        raise ValueError(f"softdtw_cuda: grad_output has {gout.numel()} elements, expected {B}")
+    if N is not None and (N == 0 or M == 0):
+        raise ValueError("softdtw_cuda: sequence lengths must be > 0")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _workspace(op, B, N, M, K, device):
+    n = int(load().sdtw_workspace_bytes(op, B, N, M, K))
+    if n == 0:
+        return None, 0
+    return torch.empty(n, dtype=torch.uint8, device=device), n
+
+
+def sqeuclid_fwd(x: torch.Tensor, y: torch.Tensor, mode: int = DIST_EXACT) -> torch.Tensor:
+    require_gpu(x, "sqeuclid x")
+    require_gpu(y, "sqeuclid y")
+    _check_shapes(x=x, y=y)
+    B, N, K = x.shape
+    M = y.shape[1]
+    D = torch.empty((B, N, M), dtype=torch.float32, device=x.device)
+    ws, nws = _workspace(OP_SQEUCLID_FWD, B, N, M, K, x.device)
+    with torch.cuda.device(x.device):
+        rc = load().sdtw_sqeuclid_fwd_f32(_ptr(x), _ptr(y), _ptr(D), B, N, M, K, int(mode),
+                                          _ptr(ws), nws, _stream(x.device))
+    _check(rc, "sqeuclid forward")
+    return D
+
+
+def sqeuclid_bwd(x, y, D, G, mask: bool = True):
+    for t, n in ((x, "x"), (y, "y"), (G, "G")):
+        require_gpu(t, f"sqeuclid backward {n}")
+    if mask:
+        require_gpu(D, "sqeuclid backward D")
+    _check_shapes(x=x, y=y, D=G)
+    if mask:
+        _check_shapes(x=x, y=y, D=D)
+    B, N, K = x.shape
+    M = y.shape[1]
+    gx = torch.empty_like(x)
+    gy = torch.empty_like(y)
+    ws, nws = _workspace(OP_SQEUCLID_BWD, B, N, M, K, x.device)
+    with torch.cuda.device(x.device):
+        rc = load().sdtw_sqeuclid_bwd_f32(_ptr(x), _ptr(y), _ptr(D if mask else None), _ptr(G),
+                                          _ptr(gx), _ptr(gy), B, N, M, K, 1 if mask else 0,
+                                          _ptr(ws), nws, _stream(x.device))
+    _check(rc, "sqeuclid backward")
+    return gx, gy
+
+
+def dtw_fwd(D: torch.Tensor, gamma: float, bandwidth: float):
+    require_gpu(D, "softdtw forward D")
+    _check_shapes(D=D)
+    B, N, M = D.shape
+    R = torch.empty((B, N, M), dtype=torch.float32, device=D.device)
+    out = torch.empty((B,), dtype=torch.float32, device=D.device)
+    ws, nws = _workspace(OP_FWD, B, N, M, 0, D.device)
+    with torch.cuda.device(D.device):
+        rc = load().sdtw_fwd_f32(_ptr(D), _ptr(R), _ptr(out), B, N, M, float(gamma),
+                                 float(bandwidth), _ptr(ws), nws, _stream(D.device))
+    _check(rc, "softdtw forward")
+    return out, R
+
+
+def dtw_bwd(D, R, gamma: float, bandwidth: float, gout=None):
+    require_gpu(D, "softdtw backward D")
+    require_gpu(R, "softdtw backward R")
+    if gout is not None:
+        require_gpu(gout, "softdtw backward grad_output")
+    _check_shapes(D=D, R=R, gout=gout)
+    B, N, M = D.shape
+    G = torch.empty((B, N, M), dtype=torch.float32, device=D.device)
+    ws, nws = _workspace(OP_BWD, B, N, M, 0, D.device)
+    with torch.cuda.device(D.device):
+        rc = load().sdtw_bwd_f32(_ptr(D), _ptr(R), _ptr(gout), _ptr(G), B, N, M, float(gamma),
+                                 float(bandwidth), _ptr(ws), nws, _stream(D.device))
+    _check(rc, "softdtw backward")
+    return G
+
+
+def fused_fwd(x, y, gamma: float, bandwidth: float):
+    require_gpu(x, "fused forward x")
+    require_gpu(y, "fused forward y")
+    _check_shapes(x=x, y=y)
+    B, N, K = x.shape
+    M = y.shape[1]
+    R = torch.empty((B, N, M), dtype=torch.float32, device=x.device)
+    out = torch.empty((B,), dtype=torch.float32, device=x.device)
+    ws, nws = _workspace(OP_FUSED_FWD, B, N, M, K, x.device)
+    with torch.cuda.device(x.device):
+        rc = load().sdtw_fused_fwd_f32(_ptr(x), _ptr(y), _ptr(R), _ptr(out), B, N, M, K,
+                                       float(gamma), float(bandwidth), _ptr(ws), nws,
+                                       _stream(x.device))
+    _check(rc, "fused forward")
+    return out, R
+
+
+def fused_bwd(x, y, R, gamma: float, bandwidth: float, gout=None):
+    require_gpu(x, "fused backward x")
+    require_gpu(y, "fused backward y")
+    require_gpu(R, "fused backward R")
+    if gout is not None:
+        require_gpu(gout, "fused backward grad_output")
+    _check_shapes(x=x, y=y, R=R, gout=gout)
+    B, N, K = x.shape
+    M = y.shape[1]
+    gx = torch.empty_like(x)
+    gy = torch.empty_like(y)
+    ws, nws = _workspace(OP_FUSED_BWD, B, N, M, K, x.device)
+    with torch.cuda.device(x.device):
+        rc = load().sdtw_fused_bwd_f32(_ptr(x), _ptr(y), _ptr(R), _ptr(gout), _ptr(gx), _ptr(gy),
+                                       B, N, M, K, float(gamma), float(bandwidth), _ptr(ws), nws,
+                                       _stream(x.device))
+    _check(rc, "fused backward")
+    return gx, gy
+
+
+def fused_bwd_e(x, y, R, gamma: float, bandwidth: float, gout=None):
+    require_gpu(x, "fused backward x")
+    require_gpu(y, "fused backward y")
+    require_gpu(R, "fused backward R")
+    if gout is not None:
+        require_gpu(gout, "fused backward grad_output")
+    _check_shapes(x=x, y=y, R=R, gout=gout)
+    B, N, K = x.shape
+    M = y.shape[1]
+    E = torch.empty((B, N, M), dtype=torch.float32, device=x.device)
+    ws, nws = _workspace(OP_FUSED_BWD, B, N, M, K, x.device)
+    with torch.cuda.device(x.device):
+        rc = load().sdtw_fused_bwd_e_f32(_ptr(x), _ptr(y), _ptr(R), _ptr(gout), _ptr(E), B, N, M,
+                                         K, float(gamma), float(bandwidth), _ptr(ws), nws,
+                                         _stream(x.device))
+    _check(rc, "fused backward (E)")
+    return E

@@ -1,0 +1,47 @@
+from __future__ import annotations
+
+import torch
+from torch.autograd import Function
+
+from . import _engine
+from ._device import compute_device, to_engine
+from .utils.checks import check_D
+
+
+def _normalize_bandwidth(bandwidth) -> float:
+    """None or <= 0 disables the band: -1.0 (reference autograd.py:19-23)."""
+    if bandwidth is None:
+        return -1.0
+    bw = float(bandwidth)
+    return -1.0 if bw <= 0 else bw
+
+
+class SoftDTWAutograd(Function):
+    """Soft-DTW over a materialised cost D (B,N,M) -> (B,).
+
+    Forward: sdtw_fwd_f32 (fp64 recursion, R stored fp32 once).  Backward:
+    sdtw_bwd_f32 returns grad_D = g * E directly (reference autograd.py:11-48)."""
+
+    @staticmethod
+    def forward(ctx, D: torch.Tensor, gamma: float, bandwidth: float | None):
+        check_D(D)
+        gamma_f = float(gamma)
+        if gamma_f <= 0:
+            raise ValueError(f"gamma must be > 0, got {gamma_f}")
+        bandwidth_f = _normalize_bandwidth(bandwidth)
+        dev = compute_device(D)
+        Dg = to_engine(D.detach(), dev)
+        out, R = _engine.dtw_fwd(Dg, gamma_f, bandwidth_f)
+        ctx.save_for_backward(Dg, R)
+        ctx.gamma = gamma_f
+        ctx.bandwidth = bandwidth_f
+        ctx.orig = (D.device, D.dtype)
+        return out.to(device=D.device, dtype=D.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        Dg, R = ctx.saved_tensors
+        g = grad_output.reshape(-1).to(device=Dg.device, dtype=torch.float32).contiguous()
+        G = _engine.dtw_bwd(Dg, R, ctx.gamma, ctx.bandwidth, gout=g)
+        dev, dt = ctx.orig
+        return G.to(device=dev, dtype=dt), None, None

@@ -1,0 +1,47 @@
+from __future__ import annotations
+
+import torch
+from torch.autograd import Function
+
+from . import _engine
+from ._device import to_engine
+from .autograd import _normalize_bandwidth
+
+
+class SoftDTWXYAutograd(Function):
+    """Fused Soft-DTW over (X, Y) with the squared-Euclidean cost recomputed per cell; no
+    (B,N,M) cost tensor is formed (reference autograd_xy.py:12-51).
+
+    Forward: sdtw_fused_fwd_f32.  Backward: sdtw_fused_bwd_f32 returns
+    grad_X = 2 (X * sum_j gE - gE Y), grad_Y = 2 (Y * sum_i gE - gE^T X), gE = g * E."""
+
+    @staticmethod
+    def forward(ctx, X: torch.Tensor, Y: torch.Tensor, gamma: float, bandwidth: float | None):
+        if not (X.is_cuda and Y.is_cuda):
+            raise ValueError("Expected CUDA tensors X and Y")
+        if X.dim() != 3 or Y.dim() != 3:
+            raise ValueError(f"Expected X,Y as (B,N,D)/(B,M,D). Got {tuple(X.shape)} and {tuple(Y.shape)}")
+        if X.shape[0] != Y.shape[0] or X.shape[2] != Y.shape[2]:
+            raise ValueError(f"Batch/features mismatch: {tuple(X.shape)} vs {tuple(Y.shape)}")
+        gamma_f = float(gamma)
+        if not gamma_f > 0:
+            raise ValueError(f"gamma must be > 0, got {gamma_f}")
+        Xg = to_engine(X.detach(), X.device)
+        Yg = to_engine(Y.detach(), X.device)
+        # forward takes the band as given (-1 for None), the backward normalised
+        # (reference autograd_xy.py:16, :22-27); both disable it for values <= 0.
+        bw_fwd = -1.0 if bandwidth is None else float(bandwidth)
+        out, R = _engine.fused_fwd(Xg, Yg, gamma_f, bw_fwd)
+        ctx.save_for_backward(Xg, Yg, R)
+        ctx.gamma = gamma_f
+        ctx.bandwidth = _normalize_bandwidth(bandwidth)
+        ctx.dtypes = (X.dtype, Y.dtype)
+        return out.to(dtype=X.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        Xg, Yg, R = ctx.saved_tensors
+        g = grad_output.reshape(-1).to(device=Xg.device, dtype=torch.float32).contiguous()
+        gx, gy = _engine.fused_bwd(Xg, Yg, R, ctx.gamma, ctx.bandwidth, gout=g)
+        dx, dy = ctx.dtypes
+        return gx.to(dtype=dx), gy.to(dtype=dy), None, None

@@ -1,0 +1,102 @@
+"""GPU Soft-DTW recursion kernels vs the CPU oracle, given identical costs.
+
+Forward: R bit-equal rate and out within rtol 1e-5.  Backward: E (= G with g = 1) within
+rtol 1e-4 / atol 1e-5 given the same D and R.  Plus the brute-force golden vectors.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _gpu_util import (FWD_RTOL, GRAD_ATOL, GRAD_RTOL, engine_R_from_oracle, grad_violation,
+                       randn_pair, say)
+from softdtw_cuda import _engine
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "bruteforce.json")
+
+
+def _golden():
+    with open(GOLDEN) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", _golden(), ids=lambda c: f"N{c['N']}M{c['M']}g{c['gamma']}bw{c['bandwidth']}")
+def test_dp_matches_bruteforce_golden(case):
+    D = torch.tensor(case["D"], dtype=torch.float32).unsqueeze(0).cuda()
+    bw = -1.0 if case["bandwidth"] is None else case["bandwidth"]
+    out, R = _engine.dtw_fwd(D, case["gamma"], bw)
+    np.testing.assert_allclose(out.item(), case["value"], rtol=2e-6, atol=1e-6)
+    E = _engine.dtw_bwd(D, R, case["gamma"], bw).cpu()[0].numpy()
+    rmax = float(R[torch.isfinite(R)].abs().max())
+    tol = max(1e-5, 8 * 2.0 ** -24 * rmax / case["gamma"])
+    np.testing.assert_allclose(E, np.array(case["E"]), rtol=tol, atol=tol)
+
+
+CASES = [
+    # B, N, M, K, gamma, bandwidth
+    (4, 64, 64, 8, 1.0, None),        # config 1
+    (2, 12, 9, 3, 1.0, None),
+    (3, 37, 53, 4, 0.5, None),
+    (2, 100, 80, 6, 0.1, 10.0),       # band, non-square
+    (2, 64, 64, 3, 0.01, None),       # sharp soft-min
+    (32, 512, 512, 64, 1.0, None),    # config 2 (headline)
+    (2, 1300, 700, 3, 1.0, None),     # N > 1024: several row blocks
+    (2, 700, 1300, 3, 0.3, 50.0),
+]
+
+
+@pytest.mark.parametrize("B,N,M,K,gamma,bw", CASES)
+def test_dp_forward_backward_vs_oracle_same_D(B, N, M, K, gamma, bw):
+    say(f"[dp] B={B} N={N} M={M} gamma={gamma} bw={bw}")
+    x, y = randn_pair(B, N, M, K, seed=B + N + M)
+    D = oracle.sqeuclidean(x, y)
+    out_o, R_o = oracle.forward(D, gamma, bw)
+    bwv = -1.0 if bw is None else bw
+    Dg = D.cuda()
+    out, R = _engine.dtw_fwd(Dg, gamma, bwv)
+    Rref = engine_R_from_oracle(R_o)
+    Rc = R.cpu()
+    same = (Rc == Rref) | (torch.isinf(Rc) & torch.isinf(Rref))
+    rate = same.double().mean().item()
+    say(f"    R bit-equal rate {rate:.6f}")
+    assert rate >= 0.999
+    torch.testing.assert_close(out.cpu(), out_o, rtol=FWD_RTOL, atol=0)
+    # backward from identical D and R
+    E_o = oracle.backward(D, R_o, gamma, bw)
+    E = _engine.dtw_bwd(Dg, Rref.cuda(), gamma, bwv).cpu()
+    v = grad_violation(E, E_o)
+    say(f"    E violation {v:.4f} (<= 1 passes)")
+    assert v <= 1.0
+    # and from the engine's own R
+    E2 = _engine.dtw_bwd(Dg, R, gamma, bwv).cpu()
+    v2 = grad_violation(E2, E_o)
+    say(f"    E (own R) violation {v2:.4f}")
+    assert v2 <= 1.0
+
+
+def test_backward_scales_by_grad_output():
+    x, y = randn_pair(3, 20, 30, 4, seed=5)
+    D = oracle.sqeuclidean(x, y).cuda()
+    out, R = _engine.dtw_fwd(D, 1.0, -1.0)
+    g = torch.tensor([0.5, -2.0, 3.0]).cuda()
+    G = _engine.dtw_bwd(D, R, 1.0, -1.0, gout=g)
+    E = _engine.dtw_bwd(D, R, 1.0, -1.0)
+    torch.testing.assert_close(G, g.view(-1, 1, 1) * E, rtol=0, atol=0)
+
+
+def test_fused_matches_unfused_kernels():
+    # fused recomputes the same cost bits: identical out / R / E
+    for (B, N, M, K) in [(3, 50, 40, 5), (2, 12, 9, 3), (2, 1100, 300, 4)]:
+        x, y = randn_pair(B, N, M, K, seed=N)
+        xg, yg = x.cuda(), y.cuda()
+        D = _engine.sqeuclid_fwd(xg, yg)
+        o1, R1 = _engine.dtw_fwd(D, 0.7, -1.0)
+        o2, R2 = _engine.fused_fwd(xg, yg, 0.7, -1.0)
+        assert torch.equal(o1, o2) and torch.equal(R1, R2)
+        E1 = _engine.dtw_bwd(D, R1, 0.7, -1.0)
+        E2 = _engine.fused_bwd_e(xg, yg, R2, 0.7, -1.0)
+        assert torch.equal(E1, E2)

@@ -1,0 +1,60 @@
+"""The C-ABI library: it exists, loads, and exports every entry point include/sdtw.h
+declares; argument validation answers without touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from softdtw_cuda import _engine
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sdtw.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sdtw_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for must in ("sdtw_fwd_f32", "sdtw_bwd_f32", "sdtw_fused_fwd_f32", "sdtw_fused_bwd_f32",
+                 "sdtw_sqeuclid_fwd_f32", "sdtw_sqeuclid_bwd_f32", "sdtw_workspace_bytes",
+                 "sdtw_strerror"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _engine.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert set(_engine.exported_symbols()) == set(_declared())
+
+
+def test_status_strings_and_version():
+    lib = _engine.load()
+    assert lib.sdtw_version() >= 1
+    assert _engine.strerror(0) == "success"
+    assert "workspace" in _engine.strerror(2)
+
+
+def test_invalid_arguments_rejected_before_launch():
+    lib = _engine.load()
+    null = ctypes.c_void_p(0)
+    # N = 0, gamma <= 0, gamma = inf: rejected by validation, no HIP call is made
+    assert lib.sdtw_fwd_f32(null, null, null, 1, 0, 4, 1.0, -1.0, null, 0, null) == 1
+    assert lib.sdtw_fwd_f32(null, null, null, 1, 4, 4, 0.0, -1.0, null, 0, null) == 1
+    assert lib.sdtw_bwd_f32(null, null, null, null, 1, 4, 4, float("inf"), -1.0, null, 0, null) == 1
+    assert lib.sdtw_fused_fwd_f32(null, null, null, null, 1, 4, 4, 0, 1.0, -1.0, null, 0, null) == 1
+    # empty batch is a no-op success
+    assert lib.sdtw_fwd_f32(null, null, null, 0, 4, 4, 1.0, -1.0, null, 0, null) == 0
+
+
+def test_workspace_sizes():
+    lib = _engine.load()
+    B, N, M, K = 32, 512, 512, 64
+    assert lib.sdtw_workspace_bytes(_engine.OP_FWD, B, N, M, K) >= 8 * B * M
+    assert lib.sdtw_workspace_bytes(_engine.OP_FUSED_BWD, B, N, M, K) >= 4 * B * N * M
+    assert lib.sdtw_workspace_bytes(99, B, N, M, K) == 0
