@@ -1,9 +1,10 @@
 """softdtw_barycenter on the engine vs the same loop on the CPU oracle (config 5 shape).
 
 Adam's first steps move every coordinate by ~lr*sign(grad), so trajectories of any two
-implementations separate after a few iterations; parity is therefore judged on (a) the
-first iteration's loss and gradient, (b) one optimiser step, and (c) the final objective
-after the full 100-iteration run."""
+implementations separate after a few iterations (a one-ulp change of the oracle's own
+initial barycenter moves its final objective by ~1e-4 relative).  Parity is therefore
+gated on (a) the first iteration's loss and gradient, (b) one optimiser step, and (c) the
+final objective of the full 100-iteration run against the oracle's own one-ulp spread."""
 import pytest
 import torch
 
@@ -38,22 +39,35 @@ def test_first_iteration_loss_and_gradient():
         assert v <= 1.0
 
 
-def test_one_step_and_final_objective():
+def test_one_step():
     X = random_walks(KSEQ, N, D, seed=0)
     one_gpu = softdtw_barycenter(X.cuda(), gamma=1.0, lr=0.1, max_iter=1, early_stopping=False).cpu()
     one_cpu = oracle.barycenter(X, gamma=1.0, lr=0.1, max_iter=1, early_stopping=False)
     v = grad_violation(one_gpu, one_cpu)
     say(f"[bary step1] violation {v:.4f}")
     assert v <= 1.0
-    full_gpu = softdtw_barycenter(X.cuda(), gamma=1.0, lr=0.1, max_iter=100, early_stopping=False).cpu()
-    full_cpu = oracle.barycenter(X, gamma=1.0, lr=0.1, max_iter=100, early_stopping=False)
+
+
+def test_final_objective_within_oracle_noise_floor():
+    # The oracle's own sensitivity: the same 100 iterations from an init perturbed by one
+    # ulp (one element, then every element).  The engine's final objective must sit within
+    # twice that spread of the oracle's (plus 1e-5 relative).
+    X = random_walks(KSEQ, N, D, seed=0)
+    init = (X * (torch.ones(KSEQ) / KSEQ).view(KSEQ, 1, 1)).sum(dim=0)
+    kw = dict(gamma=1.0, lr=0.1, max_iter=100, early_stopping=False)
+    base = oracle.barycenter(X, init=init, **kw)
+    one = init.clone()
+    one[0, 0] = torch.nextafter(one[0, 0], torch.tensor(-1e9))
+    every = torch.nextafter(init, torch.full_like(init, 1e9))
+    f_base = _objective(base, X)
+    spread = max(abs(_objective(oracle.barycenter(X, init=i, **kw), X) - f_base) for i in (one, every))
+    full_gpu = softdtw_barycenter(X.cuda(), **kw).cpu()
     f_gpu = _objective(full_gpu, X)
-    f_cpu = _objective(full_cpu, X)
-    init_obj = _objective(X.mean(dim=0), X)
-    say(f"[bary final] objective gpu {f_gpu:.7f} oracle {f_cpu:.7f} (init {init_obj:.4f}); "
-        f"max |bary diff| {(full_gpu - full_cpu).abs().max().item():.3e}")
+    init_obj = _objective(init, X)
+    say(f"[bary final] objective gpu {f_gpu:.7f} oracle {f_base:.7f} (init {init_obj:.4f}); "
+        f"oracle 1-ulp spread {spread:.4f}; max |bary diff| {(full_gpu - base).abs().max().item():.3e}")
     assert f_gpu < init_obj
-    assert abs(f_gpu - f_cpu) <= 1e-5 * abs(f_cpu)
+    assert abs(f_gpu - f_base) <= 2.0 * spread + 1e-5 * abs(f_base)
 
 
 def test_barycenter_cpu_wrapper_and_weights():
