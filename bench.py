@@ -166,6 +166,8 @@ def main(argv=None):
     ap.add_argument("--kernel", default=None,
                     help="only launch one kernel family repeatedly (for rocprofv3 runs)")
     ap.add_argument("--launches", type=int, default=20)
+    ap.add_argument("--shape", default=None,
+                    help="B,N,M,D for --kernel runs (default: the headline 32,512,512,64)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -188,6 +190,10 @@ def main(argv=None):
     Y = y.cuda()
 
     if args.kernel:
+        if args.shape:
+            B, N, M, K = (int(v) for v in args.shape.split(","))
+            xk, yk = make_inputs(B, N, M, K, seed=0)
+            X, Y = xk.cuda(), yk.cuda()
         fn = kernel_launcher(args.kernel, X, Y, gamma)
         ms = time_kernel(fn, args.launches)
         log(f"kernel {args.kernel}: {ms:.4f} ms/launch over {args.launches} launches")

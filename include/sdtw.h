@@ -17,9 +17,11 @@
  *     frees device memory.  Scratch memory comes from the caller as `ws`/`ws_bytes`
  *     (size it with sdtw_workspace_bytes).
  *   - The return value is an sdtw_status; sdtw_strerror() describes it.
- *   - R (the forward table kept for the backward) is engine-internal: fp32, (B, N, M)
- *     unpadded, row-major, R[b,i,j] = the reference's R[b,i+1,j+1] (launcher.py:177) rounded
- *     once from an fp64 recursion.  Out-of-band cells hold +inf.
+ *   - R (the forward table kept for the backward) is engine-internal: sdtw_table_elems()
+ *     fp32 values in a band-skewed layout (64-row bands, one anti-diagonal step per 64
+ *     contiguous floats).  Its cells are the reference's R[b,i+1,j+1] (launcher.py:177)
+ *     rounded once from an fp64 recursion; out-of-band cells hold +inf.  Convert with
+ *     sdtw_table_unpack_f32 / sdtw_table_pack_f32.
  *   - Re-entrant and stateless apart from a once-only device-attribute query.
  */
 #ifndef SDTW_H_
@@ -37,7 +39,8 @@ typedef enum sdtw_status {
     SDTW_ERR_INVALID_VALUE = 1,  /* bad shape, gamma, pointer */
     SDTW_ERR_WORKSPACE = 2,      /* ws too small (see sdtw_workspace_bytes) */
     SDTW_ERR_LAUNCH = 3,         /* hipLaunchKernel / runtime error */
-    SDTW_ERR_UNSUPPORTED = 4     /* shape outside what the kernels support */
+    SDTW_ERR_UNSUPPORTED = 4,    /* shape outside what the kernels support */
+    SDTW_ERR_TIMEOUT = 5         /* a bounded inter-band wait expired (results invalid) */
 } sdtw_status;
 
 /* Operation selectors for sdtw_workspace_bytes. */
@@ -64,6 +67,23 @@ typedef enum sdtw_dist_mode {
 const char *sdtw_strerror(int status);
 int sdtw_version(void);
 
+/* Diagnostic (synchronises the device): SDTW_ERR_TIMEOUT if the last wavefront launch of
+ * `op` that used workspace `ws` hit its bounded inter-band wait, else SDTW_OK.  The kernels
+ * never hang: a wait that expires raises this flag and the wave exits.  No counterpart in
+ * the reference (whose kernels have no inter-block waits). */
+int sdtw_debug_status(int op, const void *ws, size_t ws_bytes, int64_t B, int64_t N, int64_t M,
+                      int64_t K);
+
+/* Number of floats of the R table for B pairs of N x M cells. */
+int64_t sdtw_table_elems(int64_t B, int64_t N, int64_t M);
+
+/* R table -> dense (B, N, M) row-major, and back.  No counterpart in the reference, whose
+ * R is already dense (launcher.py:177); these exist for inspection and tests. */
+int sdtw_table_unpack_f32(const float *Rt, float *R, int64_t B, int64_t N, int64_t M,
+                          void *stream);
+int sdtw_table_pack_f32(const float *R, float *Rt, int64_t B, int64_t N, int64_t M,
+                        void *stream);
+
 /* Bytes of caller-provided scratch that `op` needs at this shape (0 if none). */
 size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K);
 
@@ -84,7 +104,7 @@ int sdtw_sqeuclid_bwd_f32(const float *x, const float *y, const float *D, const 
                           float *gx, float *gy, int64_t B, int64_t N, int64_t M, int64_t K,
                           int mask, void *ws, size_t ws_bytes, void *stream);
 
-/* Soft-DTW forward over a materialised cost D (B,N,M): R (B,N,M) and out[b] = R[b,N-1,M-1].
+/* Soft-DTW forward over a materialised cost D (B,N,M): R table and out[b] = R[b,N-1,M-1].
  * Replaces softdtw_cuda/cuda/launcher.py:167-223 (softdtw_forward_cuda) with the
  * numerics of the reference CPU path launcher.py:307-324 (fp64 recursion, fp32 R). */
 int sdtw_fwd_f32(const float *D, float *R, float *out, int64_t B, int64_t N, int64_t M,

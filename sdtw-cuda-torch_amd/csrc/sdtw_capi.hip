@@ -58,6 +58,63 @@ size_t ws_norms(int64_t B, int64_t N, int64_t M) {
     return align_up(sizeof(float) * B * N) + align_up(sizeof(float) * B * M);
 }
 
+// Wavefront-kernel scratch: [ticket, error flag][per-boundary counters][per-boundary rows].
+// The rows hold fp64 values (forward) or (E, R, D) float4 (backward): 16 bytes per column.
+size_t ws_dp(int64_t B, int64_t N, int64_t M) {
+    const DPGeom g = dp_geom(N);
+    return 256 + align_up(sizeof(int) * B * g.G) + align_up((size_t)16 * B * g.G * M);
+}
+
+struct DPScratch {
+    int* ticket;
+    int* err;
+    int* gflag;
+    void* gring;
+};
+
+DPScratch carve_dp(Carver& c, int64_t B, int64_t N, int64_t M) {
+    const DPGeom g = dp_geom(N);
+    DPScratch d{};
+    int* hdr = c.take<int>(64);
+    d.gflag = c.take<int>(B * g.G);
+    d.gring = c.take<unsigned char>((size_t)16 * B * g.G * M);
+    if (hdr) {
+        d.ticket = hdr;
+        d.err = hdr + 1;
+    }
+    return d;
+}
+
+void fill_dp(DPParams& p, const DPScratch& d, int64_t B, int64_t N, int64_t M, int64_t K,
+             double gamma, double bandwidth) {
+    const DPGeom g = dp_geom(N);
+    p.ticket = d.ticket;
+    p.err = d.err;
+    p.gflag = d.gflag;
+    p.gring = static_cast<double*>(d.gring);
+    p.gring4 = static_cast<float4*>(d.gring);
+    p.B = (int)B;
+    p.N = (int)N;
+    p.M = (int)M;
+    p.K = (int)K;
+    p.nb = g.nb;
+    p.W = g.W;
+    p.G = g.G;
+    p.S = dp_band_steps(M);
+    p.gamma = gamma;
+    p.inv_gamma = 1.0 / gamma;
+    p.bw = bandwidth;
+    p.ystride = 0;
+}
+
+// LDS row stride for staging y in the fused kernels (odd, so lanes reading consecutive rows
+// hit distinct banks); 0 when y of one pair does not fit next to the rings.
+int fused_ystride(int64_t M, int64_t K) {
+    const int64_t stride = (K % 2 == 0) ? K + 1 : K;
+    const int64_t bytes = M * stride * 4;
+    return bytes <= 140 * 1024 ? (int)stride : 0;
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? SDTW_OK : SDTW_ERR_LAUNCH; }
 
 }  // namespace
@@ -71,11 +128,53 @@ const char* sdtw_strerror(int status) {
         case SDTW_ERR_WORKSPACE: return "workspace too small (see sdtw_workspace_bytes)";
         case SDTW_ERR_LAUNCH: return "HIP kernel launch failed";
         case SDTW_ERR_UNSUPPORTED: return "unsupported configuration";
+        case SDTW_ERR_TIMEOUT: return "a wavefront kernel gave up waiting on a neighbour band";
         default: return "unknown sdtw status";
     }
 }
 
-int sdtw_version(void) { return 1; }
+int sdtw_version(void) { return 2; }
+
+int sdtw_debug_status(int op, const void* ws, size_t ws_bytes, int64_t B, int64_t N, int64_t M,
+                      int64_t K) {
+    (void)K;
+    if (!ws || B <= 0 || N <= 0 || M <= 0) return SDTW_ERR_INVALID_VALUE;
+    Carver c{static_cast<char*>(const_cast<void*>(ws)), ws_bytes};
+    if (op == SDTW_OP_FUSED_FWD || op == SDTW_OP_FUSED_BWD) {
+        c.take<float>(B * N);
+        c.take<float>(B * M);
+    } else if (op != SDTW_OP_FWD && op != SDTW_OP_BWD) {
+        return SDTW_OK;
+    }
+    const DPScratch d = carve_dp(c, B, N, M);
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    int flag = 0;
+    if (hipDeviceSynchronize() != hipSuccess) return SDTW_ERR_LAUNCH;
+    if (hipMemcpy(&flag, d.err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+        return SDTW_ERR_LAUNCH;
+    return flag ? SDTW_ERR_TIMEOUT : SDTW_OK;
+}
+
+int64_t sdtw_table_elems(int64_t B, int64_t N, int64_t M) {
+    if (B < 0 || N <= 0 || M <= 0) return 0;
+    return dp_table_elems(B, N, M);
+}
+
+int sdtw_table_unpack_f32(const float* Rt, float* R, int64_t B, int64_t N, int64_t M,
+                          void* stream) {
+    if (!shape_ok(B, N, M, 1, false)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!Rt || !R) return SDTW_ERR_INVALID_VALUE;
+    return status_of(launch_table_unpack(Rt, R, (int)B, (int)N, (int)M, (hipStream_t)stream));
+}
+
+int sdtw_table_pack_f32(const float* R, float* Rt, int64_t B, int64_t N, int64_t M,
+                        void* stream) {
+    if (!shape_ok(B, N, M, 1, false)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!Rt || !R) return SDTW_ERR_INVALID_VALUE;
+    return status_of(launch_table_pack(R, Rt, (int)B, (int)N, (int)M, (hipStream_t)stream));
+}
 
 size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) {
     (void)K;
@@ -85,14 +184,12 @@ size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) 
         case SDTW_OP_SQEUCLID_BWD:
             return ws_norms(B, N, M);
         case SDTW_OP_FWD:
-            return align_up(sizeof(double) * B * M);
         case SDTW_OP_BWD:
-            return align_up(sizeof(float) * B * 3 * (M + 1));
+            return ws_dp(B, N, M);
         case SDTW_OP_FUSED_FWD:
-            return ws_norms(B, N, M) + align_up(sizeof(double) * B * M);
+            return ws_norms(B, N, M) + ws_dp(B, N, M);
         case SDTW_OP_FUSED_BWD:
-            return ws_norms(B, N, M) + align_up(sizeof(float) * B * 3 * (M + 1)) +
-                   align_up(sizeof(float) * B * N * M);
+            return ws_norms(B, N, M) + ws_dp(B, N, M) + align_up(sizeof(float) * B * N * M);
         default:
             return 0;
     }
@@ -162,18 +259,13 @@ int sdtw_fwd_f32(const float* D, float* R, float* out, int64_t B, int64_t N, int
     if (B == 0) return SDTW_OK;
     if (!D || !R || !out) return SDTW_ERR_INVALID_VALUE;
     Carver c{static_cast<char*>(ws), ws_bytes};
-    FwdParams p{};
+    const DPScratch d = carve_dp(c, B, N, M);
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    DPParams p{};
+    fill_dp(p, d, B, N, M, 0, gamma, bandwidth);
     p.D = D;
     p.R = R;
     p.out = out;
-    p.edge = c.take<double>(B * M);
-    if (!c.ok) return SDTW_ERR_WORKSPACE;
-    p.B = (int)B;
-    p.N = (int)N;
-    p.M = (int)M;
-    p.K = 0;
-    p.gamma = gamma;
-    p.bw = bandwidth;
     return status_of(launch_fwd(p, false, false, (hipStream_t)stream));
 }
 
@@ -184,19 +276,14 @@ int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, in
     if (B == 0) return SDTW_OK;
     if (!D || !R || !G) return SDTW_ERR_INVALID_VALUE;
     Carver c{static_cast<char*>(ws), ws_bytes};
-    BwdParams p{};
-    p.D = D;
-    p.R = R;
-    p.gout = gout;
-    p.G = G;
-    p.edge = c.take<float>(B * 3 * (M + 1));
+    const DPScratch d = carve_dp(c, B, N, M);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
-    p.B = (int)B;
-    p.N = (int)N;
-    p.M = (int)M;
-    p.K = 0;
-    p.gamma = gamma;
-    p.bw = bandwidth;
+    DPParams p{};
+    fill_dp(p, d, B, N, M, 0, gamma, bandwidth);
+    p.D = D;
+    p.R = const_cast<float*>(R);
+    p.gout = gout;
+    p.G_out = G;
     return status_of(launch_bwd(p, false, false, (hipStream_t)stream));
 }
 
@@ -208,53 +295,43 @@ int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int
     if (!x || !y || !R || !out) return SDTW_ERR_INVALID_VALUE;
     hipStream_t st = (hipStream_t)stream;
     Carver c{static_cast<char*>(ws), ws_bytes};
-    FwdParams p{};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    p.edge = c.take<double>(B * M);
+    const DPScratch d = carve_dp(c, B, N, M);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
     if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
     if (e != hipSuccess) return SDTW_ERR_LAUNCH;
+    DPParams p{};
+    fill_dp(p, d, B, N, M, K, gamma, bandwidth);
     p.x = x;
     p.y = y;
     p.x2 = x2;
     p.y2 = y2;
     p.R = R;
     p.out = out;
-    p.B = (int)B;
-    p.N = (int)N;
-    p.M = (int)M;
-    p.K = (int)K;
-    p.gamma = gamma;
-    p.bw = bandwidth;
+    p.ystride = fused_ystride(M, K);
     return status_of(launch_fwd(p, true, small_bmm(N, M, K), st));
 }
 
 // Fused backward core: norms, then the reverse wavefront writing gout * E into `E`.
-// Workspace layout: [x2 (B*N)][y2 (B*M)][edge (B*3*(M+1))][E (B*N*M), fused grads only].
 static int fused_bwd_common(const float* x, const float* y, const float* R, const float* gout,
-                            float* E, float* x2, float* y2, float* edge, int64_t B, int64_t N,
-                            int64_t M, int64_t K, double gamma, double bandwidth,
+                            float* E, float* x2, float* y2, const DPScratch& d, int64_t B,
+                            int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
                             hipStream_t st) {
     hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
     if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
     if (e != hipSuccess) return SDTW_ERR_LAUNCH;
-    BwdParams p{};
+    DPParams p{};
+    fill_dp(p, d, B, N, M, K, gamma, bandwidth);
     p.x = x;
     p.y = y;
     p.x2 = x2;
     p.y2 = y2;
-    p.R = R;
+    p.R = const_cast<float*>(R);
     p.gout = gout;
-    p.G = E;
-    p.edge = edge;
-    p.B = (int)B;
-    p.N = (int)N;
-    p.M = (int)M;
-    p.K = (int)K;
-    p.gamma = gamma;
-    p.bw = bandwidth;
+    p.G_out = E;
+    p.ystride = fused_ystride(M, K);
     return status_of(launch_bwd(p, true, small_bmm(N, M, K), st));
 }
 
@@ -270,10 +347,10 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    float* edge = c.take<float>(B * 3 * (M + 1));
+    const DPScratch d = carve_dp(c, B, N, M);
     float* Ebuf = c.take<float>(B * N * M);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
-    int rc = fused_bwd_common(x, y, R, gout, Ebuf, x2, y2, edge, B, N, M, K, gamma, bandwidth, st);
+    int rc = fused_bwd_common(x, y, R, gout, Ebuf, x2, y2, d, B, N, M, K, gamma, bandwidth, st);
     if (rc != SDTW_OK) return rc;
     DistBwdParams q{};
     q.x = x;
@@ -302,9 +379,9 @@ int sdtw_fused_bwd_e_f32(const float* x, const float* y, const float* R, const f
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    float* edge = c.take<float>(B * 3 * (M + 1));
+    const DPScratch d = carve_dp(c, B, N, M);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
-    return fused_bwd_common(x, y, R, gout, E, x2, y2, edge, B, N, M, K, gamma, bandwidth,
+    return fused_bwd_common(x, y, R, gout, E, x2, y2, d, B, N, M, K, gamma, bandwidth,
                             (hipStream_t)stream);
 }
 

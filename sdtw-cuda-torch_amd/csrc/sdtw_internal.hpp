@@ -6,31 +6,27 @@
 
 namespace sdtw {
 
-struct FwdParams {
-    const float* D;   // unfused cost (B,N,M) or nullptr
-    const float* x;   // fused: (B,N,K)
-    const float* y;   // fused: (B,M,K)
-    const float* x2;  // fused: row norms (B,N)
-    const float* y2;  // fused: row norms (B,M)
-    float* R;         // (B,N,M)
-    float* out;       // (B)
-    double* edge;     // (B,M) fp64 hand-over between row blocks
+// Parameters of the wavefront kernels (forward and backward share one block).
+struct DPParams {
+    const float* D;     // unfused cost (B,N,M) or nullptr
+    const float* x;     // fused: (B,N,K)
+    const float* y;     // fused: (B,M,K)
+    const float* x2;    // fused: row norms (B,N)
+    const float* y2;    // fused: row norms (B,M)
+    float* R;           // band-skewed table: forward writes, backward reads
+    float* out;         // (B) forward result
+    float* G_out;       // backward: (B,N,M) = gout * E
+    const float* gout;  // backward: (B) upstream gradient or nullptr (= 1)
+    int* ticket;        // workgroup ticket counter (zeroed by the prep kernel)
+    int* gflag;         // (B*G) published-column counters of the global rings
+    double* gring;      // forward: (B*G, M) fp64 last rows
+    float4* gring4;     // backward: (B*G, M) (E, R, D, -) first rows
+    int* err;           // spin-timeout flag
     int B, N, M, K;
-    double gamma, bw;
-};
-
-struct BwdParams {
-    const float* D;
-    const float* x;
-    const float* y;
-    const float* x2;
-    const float* y2;
-    const float* R;     // (B,N,M)
-    const float* gout;  // (B) or nullptr
-    float* G;           // (B,N,M): gout * E
-    float* edge;        // (B,3,M+1) hand-over between row blocks
-    int B, N, M, K;
-    double gamma, bw;
+    int nb, W, G;       // 64-row bands per pair, waves per workgroup, workgroups per pair
+    int S;              // steps per band in the R table (dp_band_steps(M))
+    int ystride;        // fused: LDS row stride of staged y (0 = read y from global)
+    double gamma, inv_gamma, bw;
 };
 
 struct DistParams {
@@ -59,7 +55,28 @@ struct DistBwdParams {
 hipError_t launch_norms(const float* v, float* out, int64_t rows, int K, hipStream_t st);
 hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t st);
 hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st);
-hipError_t launch_fwd(const FwdParams& p, bool fused, bool muladd, hipStream_t st);
-hipError_t launch_bwd(const BwdParams& p, bool fused, bool muladd, hipStream_t st);
+hipError_t launch_fwd(const DPParams& p, bool fused, bool muladd, hipStream_t st);
+hipError_t launch_bwd(const DPParams& p, bool fused, bool muladd, hipStream_t st);
+hipError_t launch_table_unpack(const float* Rt, float* Rd, int B, int N, int M, hipStream_t st);
+hipError_t launch_table_pack(const float* Rd, float* Rt, int B, int N, int M, hipStream_t st);
+
+// Geometry of the band decomposition used by the wavefront kernels.
+struct DPGeom {
+    int nb, W, G;
+};
+inline DPGeom dp_geom(int64_t N) {
+    DPGeom g;
+    g.nb = (int)((N + 63) / 64);
+    g.W = g.nb < 4 ? g.nb : 4;
+    g.G = (g.nb + g.W - 1) / g.W;
+    return g;
+}
+// Steps of one band in the R table: the M + 63 diagonal steps rounded up to the kernels'
+// 8-step groups (the padding steps hold +inf).
+inline int dp_band_steps(int64_t M) { return (int)(((M + 63) + 7) / 8 * 8); }
+// floats in the band-skewed R table
+inline int64_t dp_table_elems(int64_t B, int64_t N, int64_t M) {
+    return B * ((N + 63) / 64) * (int64_t)dp_band_steps(M) * 64;
+}
 
 }  // namespace sdtw

@@ -14,6 +14,9 @@ import threading
 import torch
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libsdtw_hip.so")
+# SDTW_DEBUG_SYNC=1: synchronise after every wavefront launch and raise if a kernel's bounded
+# inter-band wait expired (diagnostics and tests; off by default, it costs a device sync).
+_DEBUG_SYNC = os.environ.get("SDTW_DEBUG_SYNC", "0") == "1"
 _lib = None
 _lock = threading.Lock()
 
@@ -25,6 +28,10 @@ _SIGS = {
     "sdtw_strerror": ([ctypes.c_int], ctypes.c_char_p),
     "sdtw_version": ([], ctypes.c_int),
     "sdtw_workspace_bytes": ([ctypes.c_int] + [ctypes.c_int64] * 4, ctypes.c_size_t),
+    "sdtw_table_elems": ([ctypes.c_int64] * 3, ctypes.c_int64),
+    "sdtw_debug_status": ([ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t] + [ctypes.c_int64] * 4, ctypes.c_int),
+    "sdtw_table_unpack_f32": ([ctypes.c_void_p] * 2 + [ctypes.c_int64] * 3 + [ctypes.c_void_p], ctypes.c_int),
+    "sdtw_table_pack_f32": ([ctypes.c_void_p] * 2 + [ctypes.c_int64] * 3 + [ctypes.c_void_p], ctypes.c_int),
     "sdtw_sqeuclid_fwd_f32": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4
                               + [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                               ctypes.c_int),
@@ -93,6 +100,40 @@ def require_gpu(t: torch.Tensor, what: str):
         raise RuntimeError(f"softdtw_cuda: {what} expects contiguous float32, got {t.dtype}")
 
 
+def table_elems(B, N, M) -> int:
+    """Floats in the engine's R table for B pairs of N x M cells."""
+    return int(load().sdtw_table_elems(B, N, M))
+
+
+def table_unpack(Rt: torch.Tensor, B: int, N: int, M: int) -> torch.Tensor:
+    """Engine R table -> dense (B, N, M)."""
+    require_gpu(Rt, "table")
+    if Rt.numel() != table_elems(B, N, M):
+        raise ValueError("softdtw_cuda: R table size does not match (B, N, M)")
+    R = torch.empty((B, N, M), dtype=torch.float32, device=Rt.device)
+    with torch.cuda.device(Rt.device):
+        rc = load().sdtw_table_unpack_f32(_ptr(Rt), _ptr(R), B, N, M, _stream(Rt.device))
+    _check(rc, "table unpack")
+    return R
+
+
+def table_pack(R: torch.Tensor) -> torch.Tensor:
+    """Dense (B, N, M) -> engine R table."""
+    require_gpu(R, "dense R")
+    B, N, M = R.shape
+    Rt = torch.full((table_elems(B, N, M),), float("inf"), dtype=torch.float32, device=R.device)
+    with torch.cuda.device(R.device):
+        rc = load().sdtw_table_pack_f32(_ptr(R), _ptr(Rt), B, N, M, _stream(R.device))
+    _check(rc, "table pack")
+    return Rt
+
+
+def _check_table(R, B, N, M):
+    if R.dim() != 1 or R.numel() != table_elems(B, N, M):
+        raise ValueError(f"softdtw_cuda: R must be the engine table of {table_elems(B, N, M)} "
+                         f"floats for (B,N,M)={(B, N, M)}, got shape {tuple(R.shape)}")
+
+
 def _check_shapes(x=None, y=None, D=None, R=None, gout=None):
     """Validate every operand's shape against the others before any launch: the kernels
     trust B, N, M, K."""
@@ -105,7 +146,7 @@ def _check_shapes(x=None, y=None, D=None, R=None, gout=None):
         if y.dim() != 3 or (B is not None and (y.shape[0] != B or y.shape[2] != K)):
             raise ValueError(f"softdtw_cuda: y must be (B,M,K) matching x, got {tuple(y.shape)}")
         B, M, K = y.shape
-    for name, t in (("D", D), ("R", R)):
+    for name, t in (("D", D),):
         if t is None:
             continue
         if t.dim() != 3:
@@ -114,6 +155,8 @@ def _check_shapes(x=None, y=None, D=None, R=None, gout=None):
             B, N, M = t.shape
         elif tuple(t.shape) != (B, N, M):
             raise ValueError(f"softdtw_cuda: {name} shape {tuple(t.shape)} != {(B, N, M)}")
+    if R is not None:
+        _check_table(R, B, N, M)
     if gout is not None and gout.numel() != B:
         raise ValueError(f"softdtw_cuda: grad_output has {gout.numel()} elements, expected {B}")
     if N is not None and (N == 0 or M == 0):
@@ -126,6 +169,11 @@ def _ptr(t):
 
 def _stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _debug_check(op, ws, nws, B, N, M, K, what):
+    if _DEBUG_SYNC and ws is not None:
+        _check(load().sdtw_debug_status(op, _ptr(ws), nws, B, N, M, K), what + " (debug status)")
 
 
 def _workspace(op, B, N, M, K, device):
@@ -175,13 +223,14 @@ def dtw_fwd(D: torch.Tensor, gamma: float, bandwidth: float):
     require_gpu(D, "softdtw forward D")
     _check_shapes(D=D)
     B, N, M = D.shape
-    R = torch.empty((B, N, M), dtype=torch.float32, device=D.device)
+    R = torch.empty((table_elems(B, N, M),), dtype=torch.float32, device=D.device)
     out = torch.empty((B,), dtype=torch.float32, device=D.device)
     ws, nws = _workspace(OP_FWD, B, N, M, 0, D.device)
     with torch.cuda.device(D.device):
         rc = load().sdtw_fwd_f32(_ptr(D), _ptr(R), _ptr(out), B, N, M, float(gamma),
                                  float(bandwidth), _ptr(ws), nws, _stream(D.device))
     _check(rc, "softdtw forward")
+    _debug_check(OP_FWD, ws, nws, B, N, M, 0, "softdtw forward")
     return out, R
 
 
@@ -198,6 +247,7 @@ def dtw_bwd(D, R, gamma: float, bandwidth: float, gout=None):
         rc = load().sdtw_bwd_f32(_ptr(D), _ptr(R), _ptr(gout), _ptr(G), B, N, M, float(gamma),
                                  float(bandwidth), _ptr(ws), nws, _stream(D.device))
     _check(rc, "softdtw backward")
+    _debug_check(OP_BWD, ws, nws, B, N, M, 0, "softdtw backward")
     return G
 
 
@@ -207,7 +257,7 @@ def fused_fwd(x, y, gamma: float, bandwidth: float):
     _check_shapes(x=x, y=y)
     B, N, K = x.shape
     M = y.shape[1]
-    R = torch.empty((B, N, M), dtype=torch.float32, device=x.device)
+    R = torch.empty((table_elems(B, N, M),), dtype=torch.float32, device=x.device)
     out = torch.empty((B,), dtype=torch.float32, device=x.device)
     ws, nws = _workspace(OP_FUSED_FWD, B, N, M, K, x.device)
     with torch.cuda.device(x.device):
@@ -215,6 +265,7 @@ def fused_fwd(x, y, gamma: float, bandwidth: float):
                                        float(gamma), float(bandwidth), _ptr(ws), nws,
                                        _stream(x.device))
     _check(rc, "fused forward")
+    _debug_check(OP_FUSED_FWD, ws, nws, B, N, M, K, "fused forward")
     return out, R
 
 
@@ -235,6 +286,7 @@ def fused_bwd(x, y, R, gamma: float, bandwidth: float, gout=None):
                                        B, N, M, K, float(gamma), float(bandwidth), _ptr(ws), nws,
                                        _stream(x.device))
     _check(rc, "fused backward")
+    _debug_check(OP_FUSED_BWD, ws, nws, B, N, M, K, "fused backward")
     return gx, gy
 
 
@@ -254,4 +306,5 @@ def fused_bwd_e(x, y, R, gamma: float, bandwidth: float, gout=None):
                                          K, float(gamma), float(bandwidth), _ptr(ws), nws,
                                          _stream(x.device))
     _check(rc, "fused backward (E)")
+    _debug_check(OP_FUSED_BWD, ws, nws, B, N, M, K, "fused backward (E)")
     return E

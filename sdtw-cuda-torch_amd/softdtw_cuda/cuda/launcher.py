@@ -2,8 +2,9 @@
 (softdtw_cuda/cuda/launcher.py), implemented by the HIP engine.
 
 Differences from the reference, by design:
-  * R is the engine's table: fp32 (B, N, M) unpadded, R[b,i,j] = reference R[b,i+1,j+1]
-    (launcher.py:177), rounded once from an fp64 recursion.
+  * R is the engine's table (fp32, band-skewed, see include/sdtw.h); its cells are the
+    reference's R[b,i+1,j+1] (launcher.py:177), rounded once from an fp64 recursion.
+    _engine.table_unpack(R, B, N, M) gives the dense (B, N, M) view.
   * The *_cpu functions do not run on the CPU: this engine has only the GPU
     implementation, so they stage D through the GPU and return tensors on D's device.
 """
@@ -59,10 +60,6 @@ def softdtw_backward_cuda_fused_sqeuclid(X: torch.Tensor, Y: torch.Tensor, R: to
         raise ValueError(f"Expected X,Y as (B,N,D)/(B,M,D). Got {tuple(X.shape)} and {tuple(Y.shape)}")
     if X.shape[0] != Y.shape[0] or X.shape[2] != Y.shape[2]:
         raise ValueError(f"Batch/features mismatch: {tuple(X.shape)} vs {tuple(Y.shape)}")
-    B, N, _ = X.shape
-    M = Y.shape[1]
-    if tuple(R.shape) != (B, N, M):
-        raise ValueError(f"Expected R shape {(B, N, M)}, got {tuple(R.shape)}")
     return _engine.fused_bwd_e(to_engine(X.detach(), X.device), to_engine(Y.detach(), X.device),
                                R.contiguous(), float(gamma), _bw(bandwidth))
 
@@ -71,12 +68,11 @@ def softdtw_forward_cpu(D: torch.Tensor, gamma: float, bandwidth: float):
     """launcher.py:356-361 semantics, computed by the GPU engine; returns on D's device."""
     dev = compute_device(D)
     out, R = _engine.dtw_fwd(to_engine(D.detach(), dev), float(gamma), _bw(bandwidth))
-    return out.to(D.device, D.dtype), R.to(D.device, D.dtype)
+    return out.to(D.device, D.dtype), R
 
 
 def softdtw_backward_cpu(D: torch.Tensor, R: torch.Tensor, gamma: float, bandwidth: float):
     """launcher.py:364-368 semantics, computed by the GPU engine; returns on D's device."""
     dev = compute_device(D)
-    E = _engine.dtw_bwd(to_engine(D.detach(), dev), to_engine(R.detach(), dev), float(gamma),
-                        _bw(bandwidth))
+    E = _engine.dtw_bwd(to_engine(D.detach(), dev), R, float(gamma), _bw(bandwidth))
     return E.to(D.device, D.dtype)

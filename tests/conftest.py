@@ -3,6 +3,9 @@ import sys
 
 import pytest
 
+# GPU tests check the wavefront kernels' bounded-wait flag after every launch
+os.environ.setdefault("SDTW_DEBUG_SYNC", "1")
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "sdtw-cuda-torch_amd")
 for p in (ROOT, PKG, os.path.dirname(os.path.abspath(__file__))):

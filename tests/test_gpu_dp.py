@@ -59,7 +59,7 @@ def test_dp_forward_backward_vs_oracle_same_D(B, N, M, K, gamma, bw):
     Dg = D.cuda()
     out, R = _engine.dtw_fwd(Dg, gamma, bwv)
     Rref = engine_R_from_oracle(R_o)
-    Rc = R.cpu()
+    Rc = _engine.table_unpack(R, B, N, M).cpu()
     same = (Rc == Rref) | (torch.isinf(Rc) & torch.isinf(Rref))
     rate = same.double().mean().item()
     say(f"    R bit-equal rate {rate:.6f}")
@@ -67,7 +67,7 @@ def test_dp_forward_backward_vs_oracle_same_D(B, N, M, K, gamma, bw):
     torch.testing.assert_close(out.cpu(), out_o, rtol=FWD_RTOL, atol=0)
     # backward from identical D and R
     E_o = oracle.backward(D, R_o, gamma, bw)
-    E = _engine.dtw_bwd(Dg, Rref.cuda(), gamma, bwv).cpu()
+    E = _engine.dtw_bwd(Dg, _engine.table_pack(Rref.cuda()), gamma, bwv).cpu()
     v = grad_violation(E, E_o)
     say(f"    E violation {v:.4f} (<= 1 passes)")
     assert v <= 1.0
@@ -75,6 +75,12 @@ def test_dp_forward_backward_vs_oracle_same_D(B, N, M, K, gamma, bw):
     E2 = _engine.dtw_bwd(Dg, R, gamma, bwv).cpu()
     v2 = grad_violation(E2, E_o)
     say(f"    E (own R) violation {v2:.4f}")
+    if not v2 <= 1.0:
+        bad = ~torch.isclose(E2, E_o, rtol=1e-4, atol=1e-5)
+        idx = bad.nonzero()
+        say(f"    {bad.sum().item()} bad cells; rows by band: "
+            f"{sorted(set((idx[:, 1] // 64).tolist()))[:20]}; cols {idx[:, 2].min().item()}..{idx[:, 2].max().item()}; "
+            f"pairs {sorted(set(idx[:, 0].tolist()))}; E1 vs E2 equal: {torch.equal(E, E2)}")
     assert v2 <= 1.0
 
 
