@@ -168,6 +168,9 @@ def main(argv=None):
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--shape", default=None,
                     help="B,N,M,D for --kernel runs (default: the headline 32,512,512,64)")
+    ap.add_argument("--numerics", choices=["fast", "exact"], default="exact",
+                    help="cell arithmetic of the recursions (exact = bit-identical to the "
+                         "reference CPU path)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -177,11 +180,12 @@ def main(argv=None):
 
     import torch
 
-    from softdtw_cuda import SoftDTW
+    from softdtw_cuda import SoftDTW, set_numerics
 
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         return 1
+    set_numerics(args.numerics)
 
     B, N, M, K, gamma = 32, 512, 512, 64, 1.0
     cells = B * N * M

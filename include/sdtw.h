@@ -64,8 +64,29 @@ typedef enum sdtw_dist_mode {
     SDTW_DIST_MFMA = 1
 } sdtw_dist_mode;
 
+/* Cell arithmetic of the Soft-DTW recursions (sdtw_set_numerics). */
+typedef enum sdtw_numerics {
+    /* fp64 recursion state; the soft-min's correction term and the backward's transition
+     * weights use the hardware fp32 exp2 / log2.  R is within ~1 fp32 ulp of the reference
+     * CPU path's (forward rtol 1e-5 holds); gradients are as close to an fp64 evaluation
+     * as the reference's own fp32 path is, but not within rtol 1e-4 of that path where R
+     * differences cancel (E depends on R[succ] - R[i,j] - D[succ]). */
+    SDTW_NUMERICS_FAST = 0,
+    /* The reference CPU arithmetic (launcher.py:307-353) restated with fp64-accurate
+     * exp / log: R matches the CPU path bit for bit in every tested case and E to within
+     * rare last-bit differences, so gradients meet rtol 1e-4 / atol 1e-5.  The default. */
+    SDTW_NUMERICS_EXACT = 1
+} sdtw_numerics;
+
 const char *sdtw_strerror(int status);
 int sdtw_version(void);
+
+/* Select the cell arithmetic of every later forward / backward launch in this process;
+ * returns the previous mode, or -1 (nothing changed) for an unknown mode.  The default is
+ * SDTW_NUMERICS_EXACT.  No counterpart in the reference (its CPU path is EXACT, its CUDA
+ * kernels fp32). */
+int sdtw_set_numerics(int mode);
+int sdtw_get_numerics(void);
 
 /* Diagnostic (synchronises the device): SDTW_ERR_TIMEOUT if the last wavefront launch of
  * `op` that used workspace `ws` hit its bounded inter-band wait, else SDTW_OK.  The kernels

@@ -21,7 +21,9 @@ OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(LIBDIR, "libsdtw_hip.so")
 ARCH = os.environ.get("SDTW_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["sdtw_dist.hip", "sdtw_dp.hip", "sdtw_capi.hip"]
+# every translation unit in csrc/ (the wavefront kernels are split per variant so they
+# compile in parallel)
+SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 # -ffp-contract=off: the exact-distance and DP arithmetic is order-sensitive (fmas are
 # written explicitly where wanted).  The packed-fp32 feature is switched off for all device
@@ -63,6 +65,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     os.makedirs(LIBDIR, exist_ok=True)
     objs = []
     cmds = []
+    for stale in os.listdir(OBJDIR):  # objects of removed sources must not be linked
+        if stale.endswith(".o") and stale.replace(".o", ".hip") not in SOURCES:
+            os.remove(os.path.join(OBJDIR, stale))
     for src in SOURCES:
         obj = os.path.join(OBJDIR, src.replace(".hip", ".o"))
         objs.append(obj)

@@ -4,6 +4,8 @@
 // variants and enqueueing them on the caller's stream.  No allocation, no synchronisation.
 #include <math.h>
 
+#include <atomic>
+
 #include "../../include/sdtw.h"
 #include "sdtw_internal.hpp"
 
@@ -117,6 +119,10 @@ int fused_ystride(int64_t M, int64_t K) {
 
 int status_of(hipError_t e) { return e == hipSuccess ? SDTW_OK : SDTW_ERR_LAUNCH; }
 
+// Process-wide cell arithmetic of the wavefront kernels (sdtw_set_numerics).
+std::atomic<int> g_numerics{SDTW_NUMERICS_EXACT};
+bool exact_numerics() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_EXACT; }
+
 }  // namespace
 
 extern "C" {
@@ -133,7 +139,14 @@ const char* sdtw_strerror(int status) {
     }
 }
 
-int sdtw_version(void) { return 2; }
+int sdtw_version(void) { return 3; }
+
+int sdtw_set_numerics(int mode) {
+    if (mode != SDTW_NUMERICS_FAST && mode != SDTW_NUMERICS_EXACT) return -1;
+    return g_numerics.exchange(mode);
+}
+
+int sdtw_get_numerics(void) { return g_numerics.load(); }
 
 int sdtw_debug_status(int op, const void* ws, size_t ws_bytes, int64_t B, int64_t N, int64_t M,
                       int64_t K) {
@@ -266,7 +279,7 @@ int sdtw_fwd_f32(const float* D, float* R, float* out, int64_t B, int64_t N, int
     p.D = D;
     p.R = R;
     p.out = out;
-    return status_of(launch_fwd(p, false, false, (hipStream_t)stream));
+    return status_of(launch_fwd(p, false, false, exact_numerics(), (hipStream_t)stream));
 }
 
 int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, int64_t B,
@@ -284,7 +297,7 @@ int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, in
     p.R = const_cast<float*>(R);
     p.gout = gout;
     p.G_out = G;
-    return status_of(launch_bwd(p, false, false, (hipStream_t)stream));
+    return status_of(launch_bwd(p, false, false, exact_numerics(), (hipStream_t)stream));
 }
 
 int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int64_t B,
@@ -311,7 +324,7 @@ int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int
     p.R = R;
     p.out = out;
     p.ystride = fused_ystride(M, K);
-    return status_of(launch_fwd(p, true, small_bmm(N, M, K), st));
+    return status_of(launch_fwd(p, true, small_bmm(N, M, K), exact_numerics(), st));
 }
 
 // Fused backward core: norms, then the reverse wavefront writing gout * E into `E`.
@@ -332,7 +345,7 @@ static int fused_bwd_common(const float* x, const float* y, const float* R, cons
     p.gout = gout;
     p.G_out = E;
     p.ystride = fused_ystride(M, K);
-    return status_of(launch_bwd(p, true, small_bmm(N, M, K), st));
+    return status_of(launch_bwd(p, true, small_bmm(N, M, K), exact_numerics(), st));
 }
 
 int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const float* gout,

@@ -1,0 +1,6 @@
+// Instantiates the bwd wavefront kernels, fast arithmetic, unfused cost (sdtw_dp.hpp).
+#include "sdtw_dp.hpp"
+
+namespace sdtw {
+template hipError_t launch_dp_variant<true, false, false>(const DPParams&, bool, hipStream_t);
+}  // namespace sdtw

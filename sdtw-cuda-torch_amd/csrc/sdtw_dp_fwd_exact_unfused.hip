@@ -1,0 +1,6 @@
+// Instantiates the fwd wavefront kernels, exact arithmetic, unfused cost (sdtw_dp.hpp).
+#include "sdtw_dp.hpp"
+
+namespace sdtw {
+template hipError_t launch_dp_variant<false, true, false>(const DPParams&, bool, hipStream_t);
+}  // namespace sdtw

@@ -1,0 +1,6 @@
+// Instantiates the fwd wavefront kernels, fast arithmetic, fused cost (sdtw_dp.hpp).
+#include "sdtw_dp.hpp"
+
+namespace sdtw {
+template hipError_t launch_dp_variant<false, false, true>(const DPParams&, bool, hipStream_t);
+}  // namespace sdtw

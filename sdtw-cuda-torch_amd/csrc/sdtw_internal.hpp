@@ -55,8 +55,10 @@ struct DistBwdParams {
 hipError_t launch_norms(const float* v, float* out, int64_t rows, int K, hipStream_t st);
 hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t st);
 hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st);
-hipError_t launch_fwd(const DPParams& p, bool fused, bool muladd, hipStream_t st);
-hipError_t launch_bwd(const DPParams& p, bool fused, bool muladd, hipStream_t st);
+// exact = the reference CPU arithmetic restated bit for bit; else hardware fp32 exp2/log2
+// for the soft-min terms and backward weights (fp64 recursion state either way)
+hipError_t launch_fwd(const DPParams& p, bool fused, bool muladd, bool exact, hipStream_t st);
+hipError_t launch_bwd(const DPParams& p, bool fused, bool muladd, bool exact, hipStream_t st);
 hipError_t launch_table_unpack(const float* Rt, float* Rd, int B, int N, int M, hipStream_t st);
 hipError_t launch_table_pack(const float* Rd, float* Rt, int B, int N, int M, hipStream_t st);
 

@@ -9,5 +9,7 @@ Same names, arguments, defaults and error messages as the reference package
 from .functional import softdtw
 from .module import SoftDTW
 from .barycenters import softdtw_barycenter, softdtw_barycenter_cpu
+from ._engine import get_numerics, set_numerics
 
-__all__ = ["softdtw", "SoftDTW", "softdtw_barycenter", "softdtw_barycenter_cpu"]
+__all__ = ["softdtw", "SoftDTW", "softdtw_barycenter", "softdtw_barycenter_cpu",
+           "set_numerics", "get_numerics"]

@@ -23,10 +23,13 @@ _lock = threading.Lock()
 # include/sdtw.h enums
 OP_SQEUCLID_FWD, OP_SQEUCLID_BWD, OP_FWD, OP_BWD, OP_FUSED_FWD, OP_FUSED_BWD = range(6)
 DIST_EXACT, DIST_MFMA = 0, 1
+NUMERICS = {"fast": 0, "exact": 1}
 
 _SIGS = {
     "sdtw_strerror": ([ctypes.c_int], ctypes.c_char_p),
     "sdtw_version": ([], ctypes.c_int),
+    "sdtw_set_numerics": ([ctypes.c_int], ctypes.c_int),
+    "sdtw_get_numerics": ([], ctypes.c_int),
     "sdtw_workspace_bytes": ([ctypes.c_int] + [ctypes.c_int64] * 4, ctypes.c_size_t),
     "sdtw_table_elems": ([ctypes.c_int64] * 3, ctypes.c_int64),
     "sdtw_debug_status": ([ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t] + [ctypes.c_int64] * 4, ctypes.c_int),
@@ -82,6 +85,24 @@ def load():
 
 def exported_symbols():
     return list(_SIGS)
+
+
+def set_numerics(mode: str) -> str:
+    """Select the recursions' cell arithmetic for this process; returns the previous mode.
+
+    "exact" (default): the reference CPU arithmetic with fp64-accurate exp/log; R matches
+    the CPU path bit for bit and gradients meet rtol 1e-4 / atol 1e-5 against it.
+    "fast": same fp64 state, hardware fp32 exp2/log2 for the soft-min terms and backward
+    weights; forward within ~1 fp32 ulp, gradients as accurate (against an fp64
+    evaluation) as the reference's own fp32 path, faster recursions."""
+    if mode not in NUMERICS:
+        raise ValueError(f"softdtw_cuda: numerics must be one of {sorted(NUMERICS)}, got {mode!r}")
+    prev = load().sdtw_set_numerics(NUMERICS[mode])
+    return {v: k for k, v in NUMERICS.items()}[prev]
+
+
+def get_numerics() -> str:
+    return {v: k for k, v in NUMERICS.items()}[load().sdtw_get_numerics()]
 
 
 def strerror(rc: int) -> str:

@@ -1,6 +1,7 @@
 """Helpers shared by the GPU parity tests (test infrastructure)."""
 from __future__ import annotations
 
+import contextlib
 import math
 import sys
 
@@ -55,6 +56,46 @@ def grad_violation(got, ref, rtol=GRAD_RTOL, atol=GRAD_ATOL):
     return float(((got - ref).abs() / (atol + rtol * ref.abs())).max())
 
 
+def no_less_accurate(got, ref32, ref64, margin=1.25):
+    """Gradient criterion for the fast arithmetic.
+
+    The reference CPU path rounds R to fp32 and its gradients take differences of R, so
+    they carry the path's own rounding noise: at B=32 N=M=512 D=64 its dL/dx differs from
+    the same algorithm in fp64 by ~900x the rtol 1e-4 / atol 1e-5 scale.  A result that
+    does not reproduce that noise bit for bit passes if it is within tolerance of the fp32
+    path, or no farther from the fp64 evaluation than the fp32 path is (times `margin`).
+    Returns (ok, violation vs fp32 path, violation vs fp64, fp32 path's own violation)."""
+    v32 = grad_violation(got, ref32)
+    v64 = grad_violation(got, ref64)
+    vref = grad_violation(ref32, ref64)
+    return (v32 <= 1.0 or v64 <= max(1.0, margin * vref)), v32, v64, vref
+
+
 def engine_R_from_oracle(R_pad):
     """Oracle R (B,N+2,M+2) -> engine layout (B,N,M)."""
     return R_pad[:, 1:-1, 1:-1].contiguous()
+
+
+@contextlib.contextmanager
+def numerics(mode):
+    """Run the block with the engine's cell arithmetic set to `mode` ("fast" / "exact")."""
+    from softdtw_cuda import _engine
+
+    prev = _engine.set_numerics(mode)
+    try:
+        yield
+    finally:
+        _engine.set_numerics(prev)
+
+
+def max_rel_err(got, ref):
+    """max |got - ref| / |ref| over cells where ref is finite; inf cells must match exactly."""
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    fin = torch.isfinite(ref)
+    assert torch.equal(torch.isfinite(got), fin), "finite/infinite pattern differs"
+    assert torch.equal(got[~fin], ref[~fin]), "infinite cells differ"
+    if not fin.any():
+        return 0.0
+    d = (got[fin] - ref[fin]).abs() / ref[fin].abs().clamp_min(1e-30)
+    return float(d.max())
