@@ -61,9 +61,20 @@ def algorithmic_bytes(kernel, B, N, M, K):
     }[kernel]
 
 
+COPY_BYTES = 256 * 2 ** 20  # calibration copy: 256 MiB read + 256 MiB written
+
+
 def kernel_launcher(name, xg, yg, gamma):
-    """Closure launching exactly one engine kernel family on torch's current stream."""
+    """Closure launching exactly one engine kernel family on torch's current stream
+    ("copy": a plain device copy of known size, the counter calibration)."""
+    import torch
+
     from softdtw_cuda import _engine
+
+    if name == "copy":
+        src = torch.ones(COPY_BYTES // 4, device=xg.device)
+        dst = torch.empty_like(src)
+        return lambda: dst.copy_(src)
 
     D = _engine.sqeuclid_fwd(xg, yg)
     out, R = _engine.dtw_fwd(D, gamma, -1.0)
@@ -117,6 +128,20 @@ def time_steps(step, steps, warmup):
     return ms, peak
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` at the headline shape from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or
+    None if no summary is committed."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_B32_N512_D64_traffic.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
+
+
 def cpu_baseline(x, y, gamma, budget_s=15.0):
     """The oracle (reference CPU path restated: torch-CPU distance + C DP + autograd),
     fwd+bwd over the same headline batch, on this host's cores."""
@@ -164,7 +189,8 @@ def main(argv=None):
     ap.add_argument("--mode", choices=["both", "unfused", "fused"], default="both")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", default=None,
-                    help="only launch one kernel family repeatedly (for rocprofv3 runs)")
+                    help="only launch one kernel family repeatedly (for rocprofv3 runs): "
+                         "dist_fwd, dp_fwd, dp_bwd, dist_bwd, fused_fwd, fused_bwd_e, copy")
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--shape", default=None,
                     help="B,N,M,D for --kernel runs (default: the headline 32,512,512,64)")
@@ -205,18 +231,24 @@ def main(argv=None):
 
     modes = ["unfused", "fused"] if args.mode == "both" else [args.mode]
     res = {}
-    for mode in modes:
-        sdtw = SoftDTW(gamma=gamma, fused=(mode == "fused"))
+    other = {}  # the other cell arithmetic, reported beside the headline
+    alt = "fast" if args.numerics == "exact" else "exact"
+    for arith, table in ((args.numerics, res), (alt, other)):
+        set_numerics(arith)
+        for mode in modes:
+            sdtw = SoftDTW(gamma=gamma, fused=(mode == "fused"))
 
-        def step():
-            xs = X.detach().clone().requires_grad_(True)
-            ys = Y.detach().clone().requires_grad_(True)
-            sdtw(xs, ys).sum().backward()
+            def step():
+                xs = X.detach().clone().requires_grad_(True)
+                ys = Y.detach().clone().requires_grad_(True)
+                sdtw(xs, ys).sum().backward()
 
-        log(f"[bench] mode={mode} warmup={args.warmup} steps={args.steps}")
-        ms, peak = time_steps(step, args.steps, args.warmup)
-        res[mode] = {"ms_per_step": ms, "cells_per_s": cells / (ms * 1e-3), "peak_mib": peak}
-        log(f"[bench] mode={mode} {ms:.3f} ms/step  {cells / (ms * 1e-3):.3e} cells/s  peak {peak:.1f} MiB")
+            log(f"[bench] numerics={arith} mode={mode} warmup={args.warmup} steps={args.steps}")
+            ms, peak = time_steps(step, args.steps, args.warmup)
+            table[mode] = {"ms_per_step": ms, "cells_per_s": cells / (ms * 1e-3), "peak_mib": peak}
+            log(f"[bench] numerics={arith} mode={mode} {ms:.3f} ms/step  "
+                f"{cells / (ms * 1e-3):.3e} cells/s  peak {peak:.1f} MiB")
+    set_numerics(args.numerics)
 
     # per-kernel timing (HIP events on the engine's stream) -> dominant kernel roofline
     kernels = []
@@ -229,7 +261,10 @@ def main(argv=None):
         fn = kernel_launcher(kname, X, Y, gamma)
         per[kname] = time_kernel(fn, max(5, min(args.steps, 20)))
         log(f"[bench] kernel {kname}: {per[kname]:.4f} ms/launch")
-    dom = max(per, key=per.get)
+    head_mode = "unfused" if "unfused" in res else "fused"
+    head_kernels = {"unfused": ["dist_fwd", "dp_fwd", "dp_bwd", "dist_bwd"],
+                    "fused": ["fused_fwd", "fused_bwd_e"]}[head_mode]
+    dom = max(head_kernels, key=per.get)  # dominant kernel of the step `value` measures
     abytes = algorithmic_bytes(dom, B, N, M, K)
     achieved = abytes / (per[dom] * 1e-3) / 1e9
     roofline = {
@@ -239,7 +274,7 @@ def main(argv=None):
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 6),
-        "traffic": None,
+        "traffic": measured_traffic(dom),
         "algorithmic_bytes_per_launch": abytes,
         "avg_launch_ms": round(per[dom], 5),
         "diagonal_steps_per_launch": N + M - 1,
@@ -268,8 +303,11 @@ def main(argv=None):
             "B": B, "N": N, "M": M, "D": K, "gamma": gamma,
             "value_mode": "unfused" if "unfused" in res else "fused",
         },
+        "numerics": args.numerics,
         "modes": {k: {kk: (round(vv, 4) if kk != "cells_per_s" else vv) for kk, vv in v.items()}
                   for k, v in res.items()},
+        f"modes_{alt}_numerics": {k: {kk: (round(vv, 4) if kk != "cells_per_s" else vv)
+                                      for kk, vv in v.items()} for k, v in other.items()},
         "reference_ms": {"unfused": REF_UNFUSED_MS, "fused": REF_FUSED_MS,
                          "source": "bench/softdtw_memory_benchmark.csv:13 (unstated NVIDIA GPU)"},
         "roofline": roofline,
