@@ -60,17 +60,16 @@ size_t ws_norms(int64_t B, int64_t N, int64_t M) {
     return align_up(sizeof(float) * B * N) + align_up(sizeof(float) * B * M);
 }
 
-// Wavefront-kernel scratch: [ticket, error flag][per-boundary counters][per-boundary rows].
-// The rows hold fp64 values (forward) or (E, R, D) float4 (backward): 16 bytes per column.
+// Wavefront-kernel scratch: [ticket, error flag][per-boundary rows].  The rows hold fp64
+// values (forward) or (E, R, D, tag) float4 (backward): 16 bytes per column.
 size_t ws_dp(int64_t B, int64_t N, int64_t M) {
     const DPGeom g = dp_geom(N);
-    return 256 + align_up(sizeof(int) * B * g.G) + align_up((size_t)16 * B * g.G * M);
+    return 256 + align_up((size_t)16 * B * g.G * M);
 }
 
 struct DPScratch {
     int* ticket;
     int* err;
-    int* gflag;
     void* gring;
 };
 
@@ -78,7 +77,6 @@ DPScratch carve_dp(Carver& c, int64_t B, int64_t N, int64_t M) {
     const DPGeom g = dp_geom(N);
     DPScratch d{};
     int* hdr = c.take<int>(64);
-    d.gflag = c.take<int>(B * g.G);
     d.gring = c.take<unsigned char>((size_t)16 * B * g.G * M);
     if (hdr) {
         d.ticket = hdr;
@@ -92,7 +90,6 @@ void fill_dp(DPParams& p, const DPScratch& d, int64_t B, int64_t N, int64_t M, i
     const DPGeom g = dp_geom(N);
     p.ticket = d.ticket;
     p.err = d.err;
-    p.gflag = d.gflag;
     p.gring = static_cast<double*>(d.gring);
     p.gring4 = static_cast<float4*>(d.gring);
     p.B = (int)B;
@@ -106,15 +103,6 @@ void fill_dp(DPParams& p, const DPScratch& d, int64_t B, int64_t N, int64_t M, i
     p.gamma = gamma;
     p.inv_gamma = 1.0 / gamma;
     p.bw = bandwidth;
-    p.ystride = 0;
-}
-
-// LDS row stride for staging y in the fused kernels (odd, so lanes reading consecutive rows
-// hit distinct banks); 0 when y of one pair does not fit next to the rings.
-int fused_ystride(int64_t M, int64_t K) {
-    const int64_t stride = (K % 2 == 0) ? K + 1 : K;
-    const int64_t bytes = M * stride * 4;
-    return bytes <= 140 * 1024 ? (int)stride : 0;
 }
 
 int status_of(hipError_t e) { return e == hipSuccess ? SDTW_OK : SDTW_ERR_LAUNCH; }
@@ -323,7 +311,6 @@ int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int
     p.y2 = y2;
     p.R = R;
     p.out = out;
-    p.ystride = fused_ystride(M, K);
     return status_of(launch_fwd(p, true, small_bmm(N, M, K), exact_numerics(), st));
 }
 
@@ -344,7 +331,6 @@ static int fused_bwd_common(const float* x, const float* y, const float* R, cons
     p.R = const_cast<float*>(R);
     p.gout = gout;
     p.G_out = E;
-    p.ystride = fused_ystride(M, K);
     return status_of(launch_bwd(p, true, small_bmm(N, M, K), exact_numerics(), st));
 }
 

@@ -8,9 +8,11 @@
 //   * Up-neighbours inside a band arrive from lane l-1 by a DPP wave shift (wave_shr:1);
 //     lane 0 receives the last row of the band above through a ring:
 //       - band above in the same workgroup: an LDS ring with produced/consumed counters;
-//       - band above in another workgroup: a per-boundary row in global memory, moved with
-//         device-coherent atomics and published every U columns (no back-pressure, so a
-//         producer never waits on a consumer).
+//       - band above in another workgroup: a per-boundary row in global memory holding one
+//         entry per column, reset to an "empty" signalling-NaN pattern before the launch.
+//         The producer stores each value with a device-coherent atomic and nothing else; the
+//         consumer loads a group's entries one group ahead and accepts them once none is
+//         empty.  No counter, no fence, no wait on the producer side, and no back-pressure.
 //   * A workgroup holds W <= 4 consecutive bands (one wave per SIMD); a pair spans
 //     G = ceil(nb / W) workgroups.  Workgroups draw tickets from an atomic counter and the
 //     ticket decides (pair, group), so every cross-workgroup wait is on a workgroup that
@@ -39,7 +41,7 @@
 namespace sdtw {
 
 constexpr int WAVE = 64;
-constexpr int U = 8;      // steps per group (also the global publish granularity)
+constexpr int U = 16;     // steps per group (the unit of prefetch and of band handover)
 constexpr int RS = 128;   // LDS ring slots per band boundary (power of two, multiple of U)
 constexpr unsigned kSpinLimit = 1u << 22;
 
@@ -63,20 +65,19 @@ SDTW_DEV void lds_publish(int* p, int v) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): prior LDS writes done
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-// Cross-workgroup rows: every access -- data and counter -- is an agent-scope (device
-// coherent, sc1) atomic, so no access ever hits a stale non-coherent cache line (another
-// XCD's L2, or an earlier launch that used the same workspace).  Ordering data before its
-// counter needs only the producer's own stores to have completed: publish() waits for
-// vmcnt(0) and then stores the counter.  No cache-wide writeback/invalidate is involved.
-SDTW_DEV int glb_load(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-SDTW_DEV void glb_publish(int* p, int v) {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the row's data stores have completed
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Cross-workgroup rows.  Every access is an agent-scope (device-coherent, sc1) atomic, so
+// no access hits a stale non-coherent cache line (another XCD's L2, or an earlier launch
+// that used the same workspace).  An entry not yet written holds an "empty" pattern: a
+// signalling NaN, which no arithmetic result can be (arithmetic produces quiet NaNs).  A
+// consumer therefore needs no counter: it accepts an entry once it is not empty.  64-bit
+// atomic accesses are single-copy atomic, so an entry is seen either empty or whole.
+constexpr unsigned long long kEmpty64 = 0x7FF4000000005D7Full;  // forward rows (fp64)
+constexpr unsigned kEmpty32 = 0x7FA05D7Fu;                      // backward rows: E slot
+SDTW_DEV bool row_empty(double v) { return (unsigned long long)__double_as_longlong(v) == kEmpty64; }
+// a backward entry (E, R, D, tag) is written as two 64-bit halves; the first is whole when
+// E is not empty, the second when tag (reset to 0) is not 0
+SDTW_DEV bool row_empty4(float4 v) { return __float_as_uint(v.x) == kEmpty32 || v.w == 0.0f; }
 
-// Data of the cross-workgroup rows moves with agent-scope (device-coherent) accesses, so a
-// consumer on another XCD never reads a stale cached copy, e.g. of an earlier launch that
-// used the same workspace.
 SDTW_DEV void glb_put(double* p, double v) {
     __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), (unsigned long long)__double_as_longlong(v),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -100,12 +101,12 @@ SDTW_DEV float4 glb_get4(const float4* p) {
                        __uint_as_float((unsigned)hi), __uint_as_float((unsigned)(hi >> 32)));
 }
 
-// Spin until *flag >= need.  Returns false (and raises the error flag) on timeout.
-template <bool GLOBAL>
+// Spin until the LDS counter *flag >= need.  Returns false (and raises the error flag) on
+// timeout.
 SDTW_DEV bool wait_at_least(const int* flag, int need, int& known, int* err) {
     unsigned spins = 0;
     while (known < need) {
-        known = GLOBAL ? glb_load(flag) : lds_load(flag);
+        known = lds_load(flag);
         if (known >= need) break;
         __builtin_amdgcn_s_sleep(1);
         if (++spins > kSpinLimit) {
@@ -115,6 +116,8 @@ SDTW_DEV bool wait_at_least(const int* flag, int need, int& known, int* err) {
     }
     return true;
 }
+
+SDTW_DEV void raise_timeout(int* err) { __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 // Soft-min of the three predecessors (diag R0, up R1, left R2) in fp64: the reference CPU
 // formula (launcher.py:317-322) restated around the minimum m as
@@ -183,104 +186,184 @@ SDTW_DEV float bwd_cell_hw(float rij, float En, float Rn, float Dn, float Er, fl
 }
 
 // ---------------------------------------------------------------------------------------
-// Cost providers.  load(j) returns the cost of the lane's row at column j one group before
-// it is used.  It never faults: outside the table it reads a clamped cell, whose value the
-// step then ignores (the cell is inactive).
+// Cost ring.  Every band stages the costs of its 64 rows in LDS: a ring of CR columns per
+// row (slot = column mod CR), row stride CS floats.  A provider fills one tile of TC
+// columns x 64 rows per group, one group ahead, with coalesced loads (unfused) or matrix-
+// core products (fused); lane l then reads its diagonal cell (row l, column s - l) with a
+// conflict-free ds_read (CS - 1 is odd).  The live window of a group is 64 + 2*TC columns,
+// inside CR.  Ring slots of columns outside [0, M) hold values that are never used.
+//
+// Provider interface (all lanes call each function, wave-uniform arguments), for the tile
+// at columns [c0, c0 + TC):
+//   issue(c0)        start its memory loads (into the provider's "next" registers)
+//   begin(c0)        take the issued operands and start its arithmetic (the matrix cores
+//                    run while the wave goes on with the recursion)
+//   finish(ring, c0) write it into the ring
+// Per group: begin(t), issue(t + TC), ...recursion..., finish(ring, t).
 // ---------------------------------------------------------------------------------------
+constexpr int CR = 128;  // ring columns (power of two)
+constexpr int CS = 144;  // row stride in floats: CS mod 64 = 16 (tile writes by 4-row
+                         // groups hit disjoint banks), CS - 1 odd (diagonal reads)
+constexpr int TC = U;    // tile columns per group
+
+// Unfused: the tile is read from the (B, N, M) cost.  Lane l loads column c0 + (l & 15)
+// of rows 4k + (l >> 4), k = 0..15: each load covers 4 rows x 64 contiguous bytes.
+// Indices are clamped into the table, so no load leaves it.
 struct CostD {
-    const float* Drow;  // row min(i, N-1) of this pair's (N, M) cost
-    int M;
-    SDTW_DEV void init(const DPParams& P, int p) {
+    const float* base;  // this pair's cost
+    int M, row0, N;
+    float v[16], vn[16];
+    SDTW_DEV void init(const DPParams& P, int p, int b) {
         M = P.M;
-        Drow = P.D + (int64_t)p * P.N * P.M;
+        N = P.N;
+        base = P.D + (int64_t)p * P.N * P.M;
+        row0 = b * WAVE;
     }
-    SDTW_DEV void stage(const DPParams&, int, unsigned char*) {}
-    SDTW_DEV void set_row(int i, int N) { Drow += (int64_t)(i < N ? i : N - 1) * M; }
-    SDTW_DEV float load(int j) const {
-        const int jc = min(max(j, 0), M - 1);
-        return Drow[jc];
+    SDTW_DEV void issue(int c0) {
+        const int l = threadIdx.x & (WAVE - 1);
+        const int col = min(max(c0 + (l & 15), 0), M - 1);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int row = min(row0 + 4 * k + (l >> 4), N - 1);
+            vn[k] = base[(int64_t)row * M + col];
+        }
+    }
+    SDTW_DEV void begin(int) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = vn[k];
+    }
+    SDTW_DEV void finish(float* ring, int c0) {
+        const int l = threadIdx.x & (WAVE - 1);
+        float* dst = ring + (l >> 4) * CS + ((c0 + (l & 15)) & (CR - 1));
+#pragma unroll
+        for (int k = 0; k < 16; ++k) dst[4 * k * CS] = v[k];
     }
 };
 
-// Fused cost: the exact squared-Euclidean formula recomputed per cell.  y of the pair is
-// staged in LDS when it fits (rows padded to an odd stride, so lanes reading consecutive
-// rows hit distinct banks); x of the lane's row stays in registers when K <= KX.
-template <bool MULADD, int KX>
-struct CostXY {
-    const float* x;
+// Fused: cost = max(0, (|x_i|^2 + |y_j|^2) - 2 x_i.y_j) with the dot on the matrix cores.
+// v_mfma_f32_16x16x4_f32 chained over k = 0, 4, 8, ... accumulates each output as one
+// sequential fp32 FMA chain over k (measured bit-identical on gfx950), which is the order
+// of the reference's CPU matmul, so the cost has the same bits as the materialised one.
+// The band's x rows stay in registers (A operands, 16 rows per block, 4 blocks); the tile's
+// 16 columns of y are the B operand.  KX >= K is padded with zeros (fma(0, 0, acc) = acc).
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int KX>
+struct CostMfma {
+    static constexpr int NKK = KX / 4;
     const float* y;
     const float* y2;
-    const float* x2;
-    const float* ys;  // LDS copy of y or nullptr
-    int M, K, ystride;
-    float xr[KX > 0 ? KX : 1];
-    float x2i;
-    SDTW_DEV void init(const DPParams& P, int p) {
+    int M, K;
+    float xa[4][NKK];  // A: x[row0 + 16 rb + (l & 15)][4 kk + (l >> 4)]
+    float x2o[4][4];   // norms of the output rows row0 + 16 rb + 4 (l >> 4) + r
+    float yb[NKK];     // B: y[c0 + (l & 15)][4 kk + (l >> 4)] (issued: ybn)
+    float ybn[NKK];
+    float y2c, y2n;
+    floatx4 acc[4];
+    SDTW_DEV void init(const DPParams& P, int p, int b) {
+        const int l = threadIdx.x & (WAVE - 1);
         M = P.M;
         K = P.K;
-        x = P.x + (int64_t)p * P.N * P.K;
-        y = P.y + (int64_t)p * P.M * P.K;
-        x2 = P.x2 + (int64_t)p * P.N;
-        y2 = P.y2 + (int64_t)p * P.M;
-        x2i = 0.0f;
-        ystride = P.ystride;
-        ys = nullptr;
-    }
-    // cooperative copy of y into LDS (all threads of the workgroup)
-    SDTW_DEV void stage(const DPParams& P, int p, unsigned char* smem) {
-        if (P.ystride == 0) return;
-        float* dst = reinterpret_cast<float*>(smem);
-        const float* src = P.y + (int64_t)p * P.M * P.K;
-        const int total = P.M * P.K;
-        for (int e = threadIdx.x; e < total; e += blockDim.x) {
-            const int r = e / P.K, k = e - r * P.K;
-            dst[r * P.ystride + k] = src[e];
-        }
-        ys = dst;
-    }
-    SDTW_DEV void set_row(int i, int N) {
-        const int ii = i < N ? i : N - 1;
-        x2i = x2[ii];
-        x += (int64_t)ii * K;
-        if (KX > 0) {
+        const int N = P.N, row0 = b * WAVE;
+        const float* x = P.x + (int64_t)p * N * K;
+        const float* x2 = P.x2 + (int64_t)p * N;
+        y = P.y + (int64_t)p * M * K;
+        y2 = P.y2 + (int64_t)p * M;
 #pragma unroll
-            for (int k = 0; k < KX; ++k) xr[k] = (k < K) ? x[k] : 0.0f;
+        for (int rb = 0; rb < 4; ++rb) {
+            const int row = min(row0 + 16 * rb + (l & 15), N - 1);
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk) {
+                const int k = 4 * kk + (l >> 4);
+                xa[rb][kk] = (k < K) ? x[(int64_t)row * K + k] : 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x2o[rb][r] = x2[min(row0 + 16 * rb + 4 * (l >> 4) + r, N - 1)];
         }
     }
-    SDTW_DEV float load(int j) const {
-        const int jc = min(max(j, 0), M - 1);
-        const float* yj = ys ? ys + jc * ystride : y + (int64_t)jc * K;
-        float acc = 0.0f;
-        if (KX > 0) {
+    SDTW_DEV void issue(int c0) {
+        const int l = threadIdx.x & (WAVE - 1);
+        const int col = min(max(c0 + (l & 15), 0), M - 1);
 #pragma unroll
-            for (int k = 0; k < KX; ++k) {
-                if (k < K) {
-                    if (MULADD)
-                        acc = __fadd_rn(acc, __fmul_rn(xr[k], yj[k]));
-                    else
-                        acc = __fmaf_rn(xr[k], yj[k], acc);
-                }
-            }
-        } else {
-            for (int k = 0; k < K; ++k) {
-                if (MULADD)
-                    acc = __fadd_rn(acc, __fmul_rn(x[k], yj[k]));
-                else
-                    acc = __fmaf_rn(x[k], yj[k], acc);
-            }
+        for (int kk = 0; kk < NKK; ++kk) {
+            const int k = 4 * kk + (l >> 4);
+            ybn[kk] = (k < K) ? y[(int64_t)col * K + k] : 0.0f;
         }
-        return clamp0(exact_cost_pre(x2i, y2[jc], acc));
+        y2n = y2[col];
+    }
+    SDTW_DEV void begin(int) {
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) yb[kk] = ybn[kk];
+        y2c = y2n;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) acc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+                acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[rb][kk], yb[kk], acc[rb], 0, 0, 0);
+    }
+    SDTW_DEV void finish(float* ring, int c0) {
+        const int l = threadIdx.x & (WAVE - 1);
+        float* dst = ring + 4 * (l >> 4) * CS + ((c0 + (l & 15)) & (CR - 1));
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                dst[(16 * rb + r) * CS] = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
     }
 };
 
-// shared-memory layout of the DP kernels
+// Fused fallback (features beyond the register-resident width, and the tiny problems whose
+// reference dot is ATen's multiply-then-add kernel): each lane computes its 16 tile entries
+// (the CostD entry mapping) with a scalar chain over k from memory.
+template <bool MULADD>
+struct CostScalar {
+    const float* x;
+    const float* y;
+    const float* x2;
+    const float* y2;
+    int M, N, K, row0;
+    SDTW_DEV void init(const DPParams& P, int p, int b) {
+        M = P.M;
+        N = P.N;
+        K = P.K;
+        row0 = b * WAVE;
+        x = P.x + (int64_t)p * N * K;
+        y = P.y + (int64_t)p * M * K;
+        x2 = P.x2 + (int64_t)p * N;
+        y2 = P.y2 + (int64_t)p * M;
+    }
+    SDTW_DEV void issue(int) {}
+    SDTW_DEV void begin(int) {}
+    SDTW_DEV void finish(float* ring, int c0) {
+        const int l = threadIdx.x & (WAVE - 1);
+        const int col = min(max(c0 + (l & 15), 0), M - 1);
+        const float* yj = y + (int64_t)col * K;
+        float* dst = ring + (l >> 4) * CS + ((c0 + (l & 15)) & (CR - 1));
+        for (int k4 = 0; k4 < 16; ++k4) {
+            const int row = min(row0 + 4 * k4 + (l >> 4), N - 1);
+            const float* xi = x + (int64_t)row * K;
+            float acc = 0.0f;
+            for (int k = 0; k < K; ++k)
+                acc = MULADD ? __fadd_rn(acc, __fmul_rn(xi[k], yj[k])) : __fmaf_rn(xi[k], yj[k], acc);
+            dst[4 * k4 * CS] = clamp0(exact_cost_pre(x2[row], y2[col], acc));
+        }
+    }
+};
+
+// shared-memory layout of the DP kernels: [ticket, counters][handoff rings][cost rings]
 struct Smem {
     unsigned char* base;
     int W;
+    size_t ring_bytes;  // handoff rings of all bands
     SDTW_DEV int* ticket() const { return reinterpret_cast<int*>(base); }
     SDTW_DEV int* prod() const { return reinterpret_cast<int*>(base) + 4; }
     SDTW_DEV int* cons() const { return reinterpret_cast<int*>(base) + 4 + W; }
     SDTW_DEV unsigned char* ring() const { return base + 256; }
+    SDTW_DEV float* cost_ring(int w) const {
+        return reinterpret_cast<float*>(base + 256 + ring_bytes) + (size_t)w * WAVE * CS;
+    }
 };
 
 SDTW_DEV size_t ring_bytes_fwd(int W) { return (size_t)W * RS * sizeof(double); }
@@ -300,105 +383,129 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const double c2 = inv_gamma * 1.4426950408889634074;  // log2(e) / gamma
     const double ngl = -gamma * 0.69314718055994530942;   // -gamma ln2
     const double INF = dinf();
-    cost.set_row(i, N);
 
     double* lring = reinterpret_cast<double*>(sm.ring());
+    float* cring = sm.cost_ring(w);
+    const float* crow = cring + l * CS;  // my row of the cost ring
     const bool in_glb = (b > 0) && (w == 0);  // band above in workgroup g-1 (else LDS)
     const bool out_lds = (b + 1 < nb) && (w + 1 < W);
     const bool out_glb = (b + 1 < nb) && (w + 1 == W);
     const double* gin = P.gring + ((int64_t)p * G + (g - 1)) * M;
-    const int* gin_flag = P.gflag + p * G + (g - 1);
     double* gout = P.gring + ((int64_t)p * G + g) * M;
-    int* gout_flag = P.gflag + p * G + g;
     const double* lin = lring + (w - 1) * RS;
     double* lout = lring + w * RS;
     const int* lin_flag = sm.prod() + (w - 1);
 
     float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
 
-    int known_in = 0;    // columns of the band above known to be available
-    int known_free = 0;  // columns of my ring known to be consumed (LDS producer)
+    int known_in = 0;    // columns of the band above known to be in the LDS ring
+    int known_free = 0;  // columns of my LDS ring known to be consumed
     double left = INF;
     double diag = (b == 0 && l == 0) ? 0.0 : INF;
     double prev = INF;   // this lane's value one step ago (sent to lane l+1 by DPP)
 
     double up_cur[U], up_nxt[U], hold[U];
-    float d_cur[U], d_nxt[U];
-    // ring values of columns [c0, c0 + U) for lane 0 (INF past M or for band 0)
-    auto fetch_up = [&](int c0, double* dst) -> bool {
+    float d_cur[U];
+
+    // Band above in the same workgroup: columns [c0, c0 + U) of its last row from the LDS
+    // ring, for lane 0 (+inf past M or for band 0).
+    auto fetch_lds = [&](int c0, double* dst) -> bool {
 #pragma unroll
         for (int u = 0; u < U; ++u) dst[u] = INF;
         if (b == 0 || c0 >= M) return true;
         const int need = min(c0 + U, M);
-        if (in_glb) {
-            if (!wait_at_least<true>(gin_flag, need, known_in, P.err)) return false;
+        if (!wait_at_least(lin_flag, need, known_in, P.err)) return false;
+        const double2* src = reinterpret_cast<const double2*>(lin + (c0 & (RS - 1)));
+#pragma unroll
+        for (int u = 0; u < U / 2; ++u) {
+            const double2 v = src[u];
+            dst[2 * u] = v.x;
+            dst[2 * u + 1] = v.y;
+        }
+        if (l == 0) lds_publish(sm.cons() + (w - 1), need);
+        return true;
+    };
+    // Band above in another workgroup: lane 0 loads the row entries of columns [c0, c0+U)
+    // (issued one group ahead; columns past M read as +inf) ...
+    auto glb_issue = [&](int c0, double* dst) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) dst[u] = INF;
+        if (l == 0) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 if (c0 + u < M) dst[u] = glb_get(gin + c0 + u);
-        } else {
-            if (!wait_at_least<false>(lin_flag, need, known_in, P.err)) return false;
-            const double2* src = reinterpret_cast<const double2*>(lin + (c0 & (RS - 1)));
+        }
+    };
+    // ... and accepts them once none is empty (re-reading the missing ones, bounded).
+    auto glb_accept = [&](int c0, double* v) -> bool {
+        bool miss = false;
 #pragma unroll
-            for (int u = 0; u < U / 2; ++u) {
-                const double2 v = src[u];
-                dst[2 * u] = v.x;
-                dst[2 * u + 1] = v.y;
+        for (int u = 0; u < U; ++u) miss = miss || row_empty(v[u]);
+        unsigned spins = 0;
+        while (__any(miss)) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > kSpinLimit) {
+                raise_timeout(P.err);
+                return false;
             }
-            if (l == 0) lds_publish(sm.cons() + (w - 1), need);
+            miss = false;
+            if (l == 0) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    if (row_empty(v[u])) v[u] = glb_get(gin + c0 + u);
+                    miss = miss || row_empty(v[u]);
+                }
+            }
         }
         return true;
     };
-    // hand the last row's columns written by the group at s0 (lane 63 computed column
-    // s0 + u - 63 at step s0 + u) to the band below
+    // Hand the last row's columns computed by the group at s0 (lane 63 computed column
+    // s0 + u - 63 at step s0 + u) to the band below.  The LDS writes are unconditional:
+    // slots of columns < 0 or >= M are never read before being rewritten or at all.
     auto handover = [&](int s0) {
         if (l != WAVE - 1) return;
         const int c0 = s0 - (WAVE - 1);
+        if (out_lds) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u;
-            if (c >= 0 && c < M) {
-                if (out_lds)
-                    lout[c & (RS - 1)] = hold[u];
-                else
-                    glb_put(gout + c, hold[u]);
-            }
+            for (int u = 0; u < U; ++u) lout[(c0 + u) & (RS - 1)] = hold[u];
+            lds_publish(sm.prod() + w, min(max(s0 + U - (WAVE - 1), 0), M));
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if ((unsigned)(c0 + u) < (unsigned)M) glb_put(gout + c0 + u, hold[u]);
         }
-        const int done = min(max(s0 + U - (WAVE - 1), 0), M);
-        if (out_lds)
-            lds_publish(sm.prod() + w, done);
-        else if (done > 0)
-            glb_publish(gout_flag, done);
     };
 
-    // Costs are fetched one group ahead.  Ring values from the LDS are fetched for the
-    // current group at its start; from global memory one group ahead, and a global producer
-    // publishes a group's values at the start of the next group, when everything it has
-    // in flight is old, so the publish wait is short.
-#pragma unroll
-    for (int u = 0; u < U; ++u) d_nxt[u] = cost.load(u - l);
-    if (in_glb && !fetch_up(0, up_nxt)) return;
+    // Cost tiles are staged one group ahead (tile [s0, s0+TC) is in the ring when group s0
+    // starts); cross-workgroup rows are loaded one group ahead; LDS rows are read at the
+    // start of their group.
+    cost.issue(0);
+    cost.begin(0);
+    cost.finish(cring, 0);
+    if (TC < S) cost.issue(TC);
+    if (in_glb) glb_issue(0, up_nxt);
 
     for (int s0 = 0; s0 < S; s0 += U) {
-        if (out_glb && s0 > 0) handover(s0 - U);
 #pragma unroll
-        for (int u = 0; u < U; ++u) d_cur[u] = d_nxt[u];
+        for (int u = 0; u < U; ++u) d_cur[u] = crow[(s0 + u - l) & (CR - 1)];
+        const int t1 = s0 + TC;
+        if (t1 < S) {
+            cost.begin(t1);
+            if (t1 + TC < S) cost.issue(t1 + TC);
+        }
         if (in_glb) {
+            if (!glb_accept(s0, up_nxt)) return;
 #pragma unroll
             for (int u = 0; u < U; ++u) up_cur[u] = up_nxt[u];
-        } else if (!fetch_up(s0, up_cur)) {
+        } else if (!fetch_lds(s0, up_cur)) {
             return;
         }
-        const int n0 = s0 + U;
-        if (n0 < S) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) d_nxt[u] = cost.load(n0 + u - l);
-            if (in_glb && !fetch_up(n0, up_nxt)) return;
-        }
+        if (in_glb && s0 + U < S) glb_issue(s0 + U, up_nxt);
         // this group writes columns up to s0 + U - 64 of my last row; writing column c
         // reuses the slot of column c - RS, which the consumer must have taken
         if (out_lds) {
             const int need_free = s0 + U - WAVE + 1 - RS;
-            if (need_free > 0 && !wait_at_least<false>(sm.cons() + w, need_free, known_free, P.err)) return;
+            if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err)) return;
         }
         float* Rg = Rt + (int64_t)s0 * WAVE;
 #pragma unroll
@@ -425,9 +532,9 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             hold[u] = r;
             Rg[u * WAVE] = (float)r;
         }
-        if (out_lds) handover(s0);
+        if (t1 < S) cost.finish(cring, t1);
+        if (out_lds || out_glb) handover(s0);
     }
-    if (out_glb) handover(S - U);
     // out[p] = R[N-1, M-1] as stored (step M-1+l of this lane, written by this lane)
     if (i == N - 1) P.out[p] = Rt[(int64_t)(M - 1 + l) * WAVE];
 }
@@ -435,18 +542,16 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 template <class Cost, bool BAND, bool EXACT>
 __global__ void __launch_bounds__(256) fwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    Smem sm{smem_raw, P.W};
+    Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W)};
     const int w = threadIdx.x / WAVE;
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * P.W) sm.prod()[threadIdx.x] = 0;  // prod and cons are contiguous
     __syncthreads();
     const int t = *sm.ticket();
     const int p = t / P.G, g = t - p * P.G;
-    Cost cost;
-    cost.init(P, p);
-    cost.stage(P, p, sm.ring() + ring_bytes_fwd(P.W));
-    __syncthreads();
     if (g * P.W + w >= P.nb) return;
+    Cost cost;
+    cost.init(P, p, g * P.W + w);
     fwd_band<Cost, BAND, EXACT>(P, cost, sm, p, g, w);
 }
 
@@ -473,7 +578,8 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const float c2 = (float)(inv_gamma * 1.4426950408889634074);  // log2(e) / gamma
     const float NINF = -finf();
     const float gsc = P.gout ? P.gout[p] : 1.0f;
-    cost.set_row(i, N);
+    float* cring = sm.cost_ring(w);
+    const float* crow = cring + l * CS;  // my row of the cost ring
 
     // corner R (as stored by the forward) of this pair
     const int lb = nb - 1, ll = (N - 1) - lb * WAVE;
@@ -486,9 +592,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const bool out_glb = (b > 0) && (w == 0);
     // global rows indexed by the producing group; WG g consumes what group g+1 produced
     const float4* gin = P.gring4 + ((int64_t)p * G + (g + 1)) * M;
-    const int* gin_flag = P.gflag + p * G + (g + 1);
     float4* gout = P.gring4 + ((int64_t)p * G + g) * M;
-    int* gout_flag = P.gflag + p * G + g;
     const float4* lin = lring + (w + 1) * RS;
     float4* lout = lring + w * RS;
     const int* lin_flag = sm.prod() + (w + 1);
@@ -504,84 +608,112 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     float pE = 0.0f, pR = NINF, pD = 0.0f;  // published one step ago
 
     float4 dn_cur[U], dn_nxt[U], hold[U];
-    float r_cur[U], r_nxt[U], d_cur[U], d_nxt[U];
-    const float4 pad4 = make_float4(0.0f, NINF, 0.0f, 0.0f);
-    auto fetch_dn = [&](int q0, float4* dst) -> bool {
+    float r_cur[U], r_nxt[U], d_cur[U];
+    // padding of the reference below the table and right of it (E 0, R -inf, D 0); the
+    // fourth component is the row-entry tag (non-zero = written)
+    const float4 pad4 = make_float4(0.0f, NINF, 0.0f, 1.0f);
+    // Band below in the same workgroup: sequence numbers [q0, q0 + U) of its first row
+    // from the LDS ring, for lane 63.
+    auto fetch_lds = [&](int q0, float4* dst) -> bool {
 #pragma unroll
         for (int u = 0; u < U; ++u) dst[u] = pad4;
         if (b + 1 >= nb || q0 >= M) return true;
         const int need = min(q0 + U, M);
-        if (in_glb) {
-            if (!wait_at_least<true>(gin_flag, need, known_in, P.err)) return false;
+        if (!wait_at_least(lin_flag, need, known_in, P.err)) return false;
+#pragma unroll
+        for (int u = 0; u < U; ++u) dst[u] = lin[(q0 + u) & (RS - 1)];
+        if (l == 0) lds_publish(sm.cons() + (w + 1), need);
+        return true;
+    };
+    // Band below in another workgroup: lane 63 loads the row entries of sequence numbers
+    // [q0, q0 + U), one group ahead, and accepts them once none is empty.
+    auto glb_issue = [&](int q0, float4* dst) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) dst[u] = pad4;
+        if (l == WAVE - 1) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 if (q0 + u < M) dst[u] = glb_get4(gin + q0 + u);
-        } else {
-            if (!wait_at_least<false>(lin_flag, need, known_in, P.err)) return false;
+        }
+    };
+    auto glb_accept = [&](int q0, float4* v) -> bool {
+        bool miss = false;
 #pragma unroll
-            for (int u = 0; u < U; ++u) dst[u] = lin[(q0 + u) & (RS - 1)];
-            if (l == 0) lds_publish(sm.cons() + (w + 1), need);
+        for (int u = 0; u < U; ++u) miss = miss || row_empty4(v[u]);
+        unsigned spins = 0;
+        while (__any(miss)) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > kSpinLimit) {
+                raise_timeout(P.err);
+                return false;
+            }
+            miss = false;
+            if (l == WAVE - 1) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    if (row_empty4(v[u])) v[u] = glb_get4(gin + q0 + u);
+                    miss = miss || row_empty4(v[u]);
+                }
+            }
         }
         return true;
     };
     // hand the band's first row to the band above: lane 0 produced sequence numbers
-    // q - 63 (= M - 1 - j) during the group at q0
+    // q - 63 (= M - 1 - j) during the group at q0 (LDS writes unconditional, as in the
+    // forward)
     auto handover = [&](int q0) {
         if (l != 0) return;
         const int c0 = q0 - (WAVE - 1);
+        if (out_lds) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u;
-            if (c >= 0 && c < M) {
-                if (out_lds)
-                    lout[c & (RS - 1)] = hold[u];
-                else
-                    glb_put4(gout + c, hold[u]);
-            }
+            for (int u = 0; u < U; ++u) lout[(c0 + u) & (RS - 1)] = hold[u];
+            lds_publish(sm.prod() + w, min(max(q0 + U - (WAVE - 1), 0), M));
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if ((unsigned)(c0 + u) < (unsigned)M) glb_put4(gout + c0 + u, hold[u]);
         }
-        const int done = min(max(q0 + U - (WAVE - 1), 0), M);
-        if (out_lds)
-            lds_publish(sm.prod() + w, done);
-        else if (done > 0)
-            glb_publish(gout_flag, done);
     };
     // forward step of reverse step q, clamped into the band (padding steps are inactive)
     auto fstep = [&](int q) { return max(M + 62 - q, 0); };
 
+    // cost tile of reverse group q0: columns [M - TC - q0, M - q0) (lane 63's newest)
+    auto tile_col = [&](int q0) { return M - TC - q0; };
+    cost.issue(tile_col(0));
+    cost.begin(tile_col(0));
+    cost.finish(cring, tile_col(0));
+    if (TC < S) cost.issue(tile_col(TC));
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int sf = fstep(u);
-        r_nxt[u] = Rt[(int64_t)sf * WAVE];
-        d_nxt[u] = cost.load(sf - l);
-    }
-    if (in_glb && !fetch_dn(0, dn_nxt)) return;
+    for (int u = 0; u < U; ++u) r_nxt[u] = Rt[(int64_t)fstep(u) * WAVE];
+    if (in_glb) glb_issue(0, dn_nxt);
 
     for (int q0 = 0; q0 < S; q0 += U) {
-        if (out_glb && q0 > 0) handover(q0 - U);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             r_cur[u] = r_nxt[u];
-            d_cur[u] = d_nxt[u];
+            d_cur[u] = crow[((M - 1) - (q0 + u) + (WAVE - 1 - l)) & (CR - 1)];
+        }
+        const int t1 = q0 + TC;
+        if (t1 < S) {
+            cost.begin(tile_col(t1));
+            if (t1 + TC < S) cost.issue(tile_col(t1 + TC));
         }
         if (in_glb) {
+            if (!glb_accept(q0, dn_nxt)) return;
 #pragma unroll
             for (int u = 0; u < U; ++u) dn_cur[u] = dn_nxt[u];
-        } else if (!fetch_dn(q0, dn_cur)) {
+        } else if (!fetch_lds(q0, dn_cur)) {
             return;
         }
         const int n0 = q0 + U;
         if (n0 < S) {
+            if (in_glb) glb_issue(n0, dn_nxt);
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int sf = fstep(n0 + u);
-                r_nxt[u] = Rt[(int64_t)sf * WAVE];
-                d_nxt[u] = cost.load(sf - l);
-            }
-            if (in_glb && !fetch_dn(n0, dn_nxt)) return;
+            for (int u = 0; u < U; ++u) r_nxt[u] = Rt[(int64_t)fstep(n0 + u) * WAVE];
         }
         if (out_lds) {  // as in the forward: sequence numbers up to q0 + U - 64 this group
             const int need_free = q0 + U - WAVE + 1 - RS;
-            if (need_free > 0 && !wait_at_least<false>(sm.cons() + w, need_free, known_free, P.err)) return;
+            if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err)) return;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -619,17 +751,17 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             pE = mE;
             pR = mR;
             pD = mD;
-            hold[u] = make_float4(mE, mR, mD, 0.0f);
+            hold[u] = make_float4(mE, mR, mD, 1.0f);
         }
-        if (out_lds) handover(q0);
+        if (t1 < S) cost.finish(cring, tile_col(t1));
+        if (out_lds || out_glb) handover(q0);
     }
-    if (out_glb) handover(S - U);
 }
 
 template <class Cost, bool BAND, bool EXACT>
 __global__ void __launch_bounds__(256) bwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    Smem sm{smem_raw, P.W};
+    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W)};
     const int w = threadIdx.x / WAVE;
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * P.W) sm.prod()[threadIdx.x] = 0;
@@ -637,24 +769,21 @@ __global__ void __launch_bounds__(256) bwd_kernel(DPParams P) {
     const int t = *sm.ticket();
     const int p = t / P.G;
     const int g = (P.G - 1) - (t - p * P.G);  // lowest ticket of a pair takes the bottom group
-    Cost cost;
-    cost.init(P, p);
-    cost.stage(P, p, sm.ring() + ring_bytes_bwd(P.W));
-    __syncthreads();
     if (g * P.W + w >= P.nb) return;
+    Cost cost;
+    cost.init(P, p, g * P.W + w);
     bwd_band<Cost, BAND, EXACT>(P, cost, sm, p, g, w);
 }
 
 // ---------------------------------------------------------------------------------------
-// Launch helpers (the prep kernel that zeroes the ticket, error flag and ring counters is
-// launched by launch_dp_prep, defined once in sdtw_dp.hip)
+// Launch helpers (the prep kernel that zeroes the ticket and error flag and empties the
+// cross-workgroup rows is launched by launch_dp_prep, defined once in sdtw_dp.hip)
 // ---------------------------------------------------------------------------------------
-hipError_t launch_dp_prep(const DPParams& P, hipStream_t st);
+hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st);
 
 inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
     const size_t ring = (size_t)P.W * RS * (bwd ? sizeof(float4) : sizeof(double));
-    const size_t ys = P.ystride ? (size_t)P.M * P.ystride * sizeof(float) : 0;
-    return 256 + ring + ys;
+    return 256 + ring + (size_t)P.W * WAVE * CS * sizeof(float);
 }
 
 template <class K>
@@ -665,7 +794,7 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, hipStream_t st) {
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipError_t e = launch_dp_prep(P, st);
+    hipError_t e = launch_dp_prep(P, bwd, st);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, dim3(P.B * P.G), dim3(P.W * WAVE), lds, st, P);
     return hipGetLastError();
@@ -682,22 +811,23 @@ hipError_t launch_cost(const DPParams& P, hipStream_t st) {
     }
 }
 
-// One (direction, arithmetic, cost source) family of kernels.  Fused kernels keep x of the
-// lane's row in registers, sized to the smallest power of two >= K (up to 64); wider
-// features, and the tiny problems that take the multiply-then-add dot, read x from memory.
+// One (direction, arithmetic, cost source) family of kernels.  Fused kernels take the
+// matrix-core cost tiles, with x rows in registers padded to the smallest of 4, 8, 16, 32,
+// 64 >= K; wider features, and the tiny problems whose reference dot is a multiply-then-add,
+// take the scalar tiles.
 template <bool BWD, bool EXACT, bool FUSED>
 hipError_t launch_dp_variant(const DPParams& P, bool muladd, hipStream_t st) {
     if constexpr (!FUSED) {
         (void)muladd;
         return launch_cost<CostD, BWD, EXACT>(P, st);
     } else {
-        if (muladd) return launch_cost<CostXY<true, 0>, BWD, EXACT>(P, st);
-        if (P.K <= 4) return launch_cost<CostXY<false, 4>, BWD, EXACT>(P, st);
-        if (P.K <= 8) return launch_cost<CostXY<false, 8>, BWD, EXACT>(P, st);
-        if (P.K <= 16) return launch_cost<CostXY<false, 16>, BWD, EXACT>(P, st);
-        if (P.K <= 32) return launch_cost<CostXY<false, 32>, BWD, EXACT>(P, st);
-        if (P.K <= 64) return launch_cost<CostXY<false, 64>, BWD, EXACT>(P, st);
-        return launch_cost<CostXY<false, 0>, BWD, EXACT>(P, st);
+        if (muladd) return launch_cost<CostScalar<true>, BWD, EXACT>(P, st);
+        if (P.K <= 4) return launch_cost<CostMfma<4>, BWD, EXACT>(P, st);
+        if (P.K <= 8) return launch_cost<CostMfma<8>, BWD, EXACT>(P, st);
+        if (P.K <= 16) return launch_cost<CostMfma<16>, BWD, EXACT>(P, st);
+        if (P.K <= 32) return launch_cost<CostMfma<32>, BWD, EXACT>(P, st);
+        if (P.K <= 64) return launch_cost<CostMfma<64>, BWD, EXACT>(P, st);
+        return launch_cost<CostScalar<false>, BWD, EXACT>(P, st);
     }
 }
 

@@ -18,14 +18,12 @@ struct DPParams {
     float* G_out;       // backward: (B,N,M) = gout * E
     const float* gout;  // backward: (B) upstream gradient or nullptr (= 1)
     int* ticket;        // workgroup ticket counter (zeroed by the prep kernel)
-    int* gflag;         // (B*G) published-column counters of the global rings
-    double* gring;      // forward: (B*G, M) fp64 last rows
-    float4* gring4;     // backward: (B*G, M) (E, R, D, -) first rows
+    double* gring;      // forward: (B*G, M) fp64 last rows of each workgroup's bands
+    float4* gring4;     // backward: (B*G, M) (E, R, D, tag) first rows
     int* err;           // spin-timeout flag
     int B, N, M, K;
     int nb, W, G;       // 64-row bands per pair, waves per workgroup, workgroups per pair
     int S;              // steps per band in the R table (dp_band_steps(M))
-    int ystride;        // fused: LDS row stride of staged y (0 = read y from global)
     double gamma, inv_gamma, bw;
 };
 
@@ -74,8 +72,8 @@ inline DPGeom dp_geom(int64_t N) {
     return g;
 }
 // Steps of one band in the R table: the M + 63 diagonal steps rounded up to the kernels'
-// 8-step groups (the padding steps hold +inf).
-inline int dp_band_steps(int64_t M) { return (int)(((M + 63) + 7) / 8 * 8); }
+// 16-step groups (the padding steps hold +inf).
+inline int dp_band_steps(int64_t M) { return (int)(((M + 63) + 15) / 16 * 16); }
 // floats in the band-skewed R table
 inline int64_t dp_table_elems(int64_t B, int64_t N, int64_t M) {
     return B * ((N + 63) / 64) * (int64_t)dp_band_steps(M) * 64;
