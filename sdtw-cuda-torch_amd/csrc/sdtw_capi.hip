@@ -64,7 +64,7 @@ size_t ws_norms(int64_t B, int64_t N, int64_t M) {
 // values (forward) or (E, R, D, tag) float4 (backward): 16 bytes per column.
 size_t ws_dp(int64_t B, int64_t N, int64_t M) {
     const DPGeom g = dp_geom(N);
-    return 256 + align_up((size_t)16 * B * g.G * M);
+    return 256 + align_up((size_t)16 * B * g.G * dp_row_entries(M));
 }
 
 struct DPScratch {
@@ -77,7 +77,7 @@ DPScratch carve_dp(Carver& c, int64_t B, int64_t N, int64_t M) {
     const DPGeom g = dp_geom(N);
     DPScratch d{};
     int* hdr = c.take<int>(64);
-    d.gring = c.take<unsigned char>((size_t)16 * B * g.G * M);
+    d.gring = c.take<unsigned char>((size_t)16 * B * g.G * dp_row_entries(M));
     if (hdr) {
         d.ticket = hdr;
         d.err = hdr + 1;
@@ -100,6 +100,7 @@ void fill_dp(DPParams& p, const DPScratch& d, int64_t B, int64_t N, int64_t M, i
     p.W = g.W;
     p.G = g.G;
     p.S = dp_band_steps(M);
+    p.RW = (int)dp_row_entries(M);
     p.gamma = gamma;
     p.inv_gamma = 1.0 / gamma;
     p.bw = bandwidth;

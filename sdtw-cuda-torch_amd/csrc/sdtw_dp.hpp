@@ -44,6 +44,7 @@ constexpr int WAVE = 64;
 constexpr int U = 16;     // steps per group (the unit of prefetch and of band handover)
 constexpr int RS = 128;   // LDS ring slots per band boundary (power of two, multiple of U)
 constexpr unsigned kSpinLimit = 1u << 22;
+constexpr int RPAD = 64;  // padding entries on each side of a cross-workgroup row
 
 // ---------------------------------------------------------------------------------------
 // wave-level helpers
@@ -100,6 +101,10 @@ SDTW_DEV float4 glb_get4(const float4* p) {
     return make_float4(__uint_as_float((unsigned)lo), __uint_as_float((unsigned)(lo >> 32)),
                        __uint_as_float((unsigned)hi), __uint_as_float((unsigned)(hi >> 32)));
 }
+SDTW_DEV double glb_get_entry(const double* p) { return glb_get(p); }
+SDTW_DEV float4 glb_get_entry(const float4* p) { return glb_get4(p); }
+SDTW_DEV bool entry_empty(double v) { return row_empty(v); }
+SDTW_DEV bool entry_empty(float4 v) { return row_empty4(v); }
 
 // Spin until the LDS counter *flag >= need.  Returns false (and raises the error flag) on
 // timeout.
@@ -195,11 +200,12 @@ SDTW_DEV float bwd_cell_hw(float rij, float En, float Rn, float Dn, float Er, fl
 //
 // Provider interface (all lanes call each function, wave-uniform arguments), for the tile
 // at columns [c0, c0 + TC):
-//   issue(c0)        start its memory loads (into the provider's "next" registers)
-//   begin(c0)        take the issued operands and start its arithmetic (the matrix cores
-//                    run while the wave goes on with the recursion)
-//   finish(ring, c0) write it into the ring
-// Per group: begin(t), issue(t + TC), ...recursion..., finish(ring, t).
+//   issue(c0)        start its memory loads
+//   begin(ring, c0)  use the loaded operands: write the tile (loads) or start its
+//                    arithmetic (matrix cores, which run while the wave goes on with the
+//                    recursion); the next issue() may then reuse the operand registers
+//   finish(ring, c0) complete it in the ring (matrix cores; no-op otherwise)
+// Per group: begin(t), issue(t + TC) a few steps later, ...recursion..., finish(t).
 // ---------------------------------------------------------------------------------------
 constexpr int CR = 128;  // ring columns (power of two)
 constexpr int CS = 144;  // row stride in floats: CS mod 64 = 16 (tile writes by 4-row
@@ -212,7 +218,7 @@ constexpr int TC = U;    // tile columns per group
 struct CostD {
     const float* base;  // this pair's cost
     int M, row0, N;
-    float v[16], vn[16];
+    float v[16];
     SDTW_DEV void init(const DPParams& P, int p, int b) {
         M = P.M;
         N = P.N;
@@ -225,19 +231,16 @@ struct CostD {
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             const int row = min(row0 + 4 * k + (l >> 4), N - 1);
-            vn[k] = base[(int64_t)row * M + col];
+            v[k] = base[(int64_t)row * M + col];
         }
     }
-    SDTW_DEV void begin(int) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = vn[k];
-    }
-    SDTW_DEV void finish(float* ring, int c0) {
+    SDTW_DEV void begin(float* ring, int c0) {
         const int l = threadIdx.x & (WAVE - 1);
         float* dst = ring + (l >> 4) * CS + ((c0 + (l & 15)) & (CR - 1));
 #pragma unroll
         for (int k = 0; k < 16; ++k) dst[4 * k * CS] = v[k];
     }
+    SDTW_DEV void finish(float*, int) {}
 };
 
 // Fused: cost = max(0, (|x_i|^2 + |y_j|^2) - 2 x_i.y_j) with the dot on the matrix cores.
@@ -256,9 +259,8 @@ struct CostMfma {
     int M, K;
     float xa[4][NKK];  // A: x[row0 + 16 rb + (l & 15)][4 kk + (l >> 4)]
     float x2o[4][4];   // norms of the output rows row0 + 16 rb + 4 (l >> 4) + r
-    float yb[NKK];     // B: y[c0 + (l & 15)][4 kk + (l >> 4)] (issued: ybn)
-    float ybn[NKK];
-    float y2c, y2n;
+    float yb[NKK];     // B: y[c0 + (l & 15)][4 kk + (l >> 4)]
+    float y2n, y2c;    // norm of the issued / the begun tile's column
     floatx4 acc[4];
     SDTW_DEV void init(const DPParams& P, int p, int b) {
         const int l = threadIdx.x & (WAVE - 1);
@@ -287,13 +289,11 @@ struct CostMfma {
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
             const int k = 4 * kk + (l >> 4);
-            ybn[kk] = (k < K) ? y[(int64_t)col * K + k] : 0.0f;
+            yb[kk] = (k < K) ? y[(int64_t)col * K + k] : 0.0f;
         }
         y2n = y2[col];
     }
-    SDTW_DEV void begin(int) {
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) yb[kk] = ybn[kk];
+    SDTW_DEV void begin(float*, int) {
         y2c = y2n;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) acc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -335,7 +335,7 @@ struct CostScalar {
         y2 = P.y2 + (int64_t)p * M;
     }
     SDTW_DEV void issue(int) {}
-    SDTW_DEV void begin(int) {}
+    SDTW_DEV void begin(float*, int) {}
     SDTW_DEV void finish(float* ring, int c0) {
         const int l = threadIdx.x & (WAVE - 1);
         const int col = min(max(c0 + (l & 15), 0), M - 1);
@@ -352,22 +352,24 @@ struct CostScalar {
     }
 };
 
-// shared-memory layout of the DP kernels: [ticket, counters][handoff rings][cost rings]
+// shared-memory layout of the DP kernels: [ticket, counters][handoff rings][cost rings];
+// W + 1 produced/consumed counter pairs, one per handoff ring
 struct Smem {
     unsigned char* base;
     int W;
     size_t ring_bytes;  // handoff rings of all bands
     SDTW_DEV int* ticket() const { return reinterpret_cast<int*>(base); }
     SDTW_DEV int* prod() const { return reinterpret_cast<int*>(base) + 4; }
-    SDTW_DEV int* cons() const { return reinterpret_cast<int*>(base) + 4 + W; }
+    SDTW_DEV int* cons() const { return reinterpret_cast<int*>(base) + 4 + (W + 1); }
     SDTW_DEV unsigned char* ring() const { return base + 256; }
     SDTW_DEV float* cost_ring(int w) const {
         return reinterpret_cast<float*>(base + 256 + ring_bytes) + (size_t)w * WAVE * CS;
     }
 };
 
-SDTW_DEV size_t ring_bytes_fwd(int W) { return (size_t)W * RS * sizeof(double); }
-SDTW_DEV size_t ring_bytes_bwd(int W) { return (size_t)W * RS * sizeof(float4); }
+// W + 1 handoff rings: one per band plus the helper wave's
+SDTW_HD size_t ring_bytes_fwd(int W) { return (size_t)(W + 1) * RS * sizeof(double); }
+SDTW_HD size_t ring_bytes_bwd(int W) { return (size_t)(W + 1) * RS * sizeof(float4); }
 
 // ---------------------------------------------------------------------------------------
 // Forward
@@ -387,14 +389,15 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     double* lring = reinterpret_cast<double*>(sm.ring());
     float* cring = sm.cost_ring(w);
     const float* crow = cring + l * CS;  // my row of the cost ring
-    const bool in_glb = (b > 0) && (w == 0);  // band above in workgroup g-1 (else LDS)
+    // LDS ring k carries the input of band k of this workgroup: ring 0 is filled by the
+    // workgroup's helper wave from the previous workgroup, ring k > 0 by band k - 1.
     const bool out_lds = (b + 1 < nb) && (w + 1 < W);
     const bool out_glb = (b + 1 < nb) && (w + 1 == W);
-    const double* gin = P.gring + ((int64_t)p * G + (g - 1)) * M;
-    double* gout = P.gring + ((int64_t)p * G + g) * M;
-    const double* lin = lring + (w - 1) * RS;
-    double* lout = lring + w * RS;
-    const int* lin_flag = sm.prod() + (w - 1);
+    // cross-workgroup row of this workgroup: RW = M + 2*RPAD entries, column c at RPAD + c
+    double* gout = P.gring + ((int64_t)p * G + g) * P.RW + RPAD;
+    const double* lin = lring + w * RS;
+    double* lout = lring + (w + 1) * RS;
+    const int* lin_flag = sm.prod() + w;
 
     float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
 
@@ -404,11 +407,11 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     double diag = (b == 0 && l == 0) ? 0.0 : INF;
     double prev = INF;   // this lane's value one step ago (sent to lane l+1 by DPP)
 
-    double up_cur[U], up_nxt[U], hold[U];
-    float d_cur[U];
+    double up_cur[U], hold[U];
+    float d_cur[U], d_nxt[U];
 
-    // Band above in the same workgroup: columns [c0, c0 + U) of its last row from the LDS
-    // ring, for lane 0 (+inf past M or for band 0).
+    // Band above: columns [c0, c0 + U) of its last row from the LDS ring, for lane 0
+    // (+inf past M or for band 0).
     auto fetch_lds = [&](int c0, double* dst) -> bool {
 #pragma unroll
         for (int u = 0; u < U; ++u) dst[u] = INF;
@@ -422,41 +425,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             dst[2 * u] = v.x;
             dst[2 * u + 1] = v.y;
         }
-        if (l == 0) lds_publish(sm.cons() + (w - 1), need);
-        return true;
-    };
-    // Band above in another workgroup: lane 0 loads the row entries of columns [c0, c0+U)
-    // (issued one group ahead; columns past M read as +inf) ...
-    auto glb_issue = [&](int c0, double* dst) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) dst[u] = INF;
-        if (l == 0) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (c0 + u < M) dst[u] = glb_get(gin + c0 + u);
-        }
-    };
-    // ... and accepts them once none is empty (re-reading the missing ones, bounded).
-    auto glb_accept = [&](int c0, double* v) -> bool {
-        bool miss = false;
-#pragma unroll
-        for (int u = 0; u < U; ++u) miss = miss || row_empty(v[u]);
-        unsigned spins = 0;
-        while (__any(miss)) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > kSpinLimit) {
-                raise_timeout(P.err);
-                return false;
-            }
-            miss = false;
-            if (l == 0) {
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    if (row_empty(v[u])) v[u] = glb_get(gin + c0 + u);
-                    miss = miss || row_empty(v[u]);
-                }
-            }
-        }
+        if (l == 0) lds_publish(sm.cons() + w, need);
         return true;
     };
     // Hand the last row's columns computed by the group at s0 (lane 63 computed column
@@ -468,44 +437,41 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         if (out_lds) {
 #pragma unroll
             for (int u = 0; u < U; ++u) lout[(c0 + u) & (RS - 1)] = hold[u];
-            lds_publish(sm.prod() + w, min(max(s0 + U - (WAVE - 1), 0), M));
+            lds_publish(sm.prod() + (w + 1), min(max(s0 + U - (WAVE - 1), 0), M));
         } else {
+            // columns in [-63, M + 15]: inside the row's padding, no test needed
 #pragma unroll
-            for (int u = 0; u < U; ++u)
-                if ((unsigned)(c0 + u) < (unsigned)M) glb_put(gout + c0 + u, hold[u]);
+            for (int u = 0; u < U; ++u) glb_put(gout + c0 + u, hold[u]);
         }
     };
 
-    // Cost tiles are staged one group ahead (tile [s0, s0+TC) is in the ring when group s0
-    // starts); cross-workgroup rows are loaded one group ahead; LDS rows are read at the
-    // start of their group.
+    // Pipeline of one group (all of it straight-line code between the waits):
+    //   - costs of this group were read from the ring during the previous group;
+    //   - the tile two groups ahead takes its operands (begin), the one three groups ahead
+    //     starts loading (issue, after step 3), and the tile two ahead lands in the ring
+    //     (finish, after the last step), so the ring holds tiles up to s0 + 2*TC;
+    //   - the band above's row is read from the LDS ring at the group start.
+    // Tiles past the table are harmless: loads are clamped and their slots are not live.
     cost.issue(0);
-    cost.begin(0);
+    cost.begin(cring, 0);
     cost.finish(cring, 0);
-    if (TC < S) cost.issue(TC);
-    if (in_glb) glb_issue(0, up_nxt);
+    cost.issue(TC);
+    cost.begin(cring, TC);
+    cost.finish(cring, TC);
+    cost.issue(2 * TC);
+#pragma unroll
+    for (int u = 0; u < U; ++u) d_nxt[u] = crow[(u - l) & (CR - 1)];
 
     for (int s0 = 0; s0 < S; s0 += U) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) d_cur[u] = crow[(s0 + u - l) & (CR - 1)];
-        const int t1 = s0 + TC;
-        if (t1 < S) {
-            cost.begin(t1);
-            if (t1 + TC < S) cost.issue(t1 + TC);
-        }
-        if (in_glb) {
-            if (!glb_accept(s0, up_nxt)) return;
-#pragma unroll
-            for (int u = 0; u < U; ++u) up_cur[u] = up_nxt[u];
-        } else if (!fetch_lds(s0, up_cur)) {
-            return;
-        }
-        if (in_glb && s0 + U < S) glb_issue(s0 + U, up_nxt);
+        for (int u = 0; u < U; ++u) d_cur[u] = d_nxt[u];
+        cost.begin(cring, s0 + 2 * TC);
+        if (!fetch_lds(s0, up_cur)) return;
         // this group writes columns up to s0 + U - 64 of my last row; writing column c
         // reuses the slot of column c - RS, which the consumer must have taken
         if (out_lds) {
             const int need_free = s0 + U - WAVE + 1 - RS;
-            if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err)) return;
+            if (need_free > 0 && !wait_at_least(sm.cons() + (w + 1), need_free, known_free, P.err)) return;
         }
         float* Rg = Rt + (int64_t)s0 * WAVE;
 #pragma unroll
@@ -531,24 +497,72 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             prev = r;
             hold[u] = r;
             Rg[u * WAVE] = (float)r;
+            // next group's costs, and the tile work, between the steps
+            d_nxt[u] = crow[(s0 + TC + u - l) & (CR - 1)];
+            if (u == 3) cost.issue(s0 + 3 * TC);
         }
-        if (t1 < S) cost.finish(cring, t1);
+        cost.finish(cring, s0 + 2 * TC);
         if (out_lds || out_glb) handover(s0);
     }
     // out[p] = R[N-1, M-1] as stored (step M-1+l of this lane, written by this lane)
     if (i == N - 1) P.out[p] = Rt[(int64_t)(M - 1 + l) * WAVE];
 }
 
+// Helper wave of a workgroup with a band boundary above (forward) or below (backward) it
+// in another workgroup.  It polls that workgroup's cross-workgroup row, 64 entries per load,
+// copies the leading entries already written into LDS ring `k` and publishes them through
+// the ring's counter, exactly like an in-workgroup producer band.  The compute waves thus
+// never wait on global memory they did not load themselves.  Back-pressure as for a band:
+// entry e reuses the slot of e - RS, which the consumer must have taken.  Bounded: a poll
+// that finds nothing new sleeps, and too many in a row raise the timeout flag.
+template <class T>
+SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k) {
+    const int l = threadIdx.x & (WAVE - 1);
+    const int M = P.M;
+    T* ring = reinterpret_cast<T*>(sm.ring()) + k * RS;
+    int known_free = 0;
+    unsigned spins = 0;
+    for (int c = 0; c < M;) {
+        const int need_free = c + WAVE - RS;
+        if (need_free > 0 && !wait_at_least(sm.cons() + k, need_free, known_free, P.err)) return;
+        const int e = c + l;
+        T v;
+        bool empty = false;
+        if (e < M) {
+            v = glb_get_entry(gin + e);
+            empty = entry_empty(v);
+        }
+        const unsigned long long miss = __ballot(empty);
+        const int n = miss ? (int)__builtin_ctzll(miss) : WAVE;  // leading written entries
+        if (l < n && e < M) ring[e & (RS - 1)] = v;
+        if (n > 0) {
+            c = min(c + n, M);
+            if (l == 0) lds_publish(sm.prod() + k, c);
+            spins = 0;
+        } else {
+            __builtin_amdgcn_s_sleep(2);
+            if (++spins > kSpinLimit) {
+                raise_timeout(P.err);
+                return;
+            }
+        }
+    }
+}
+
 template <class Cost, bool BAND, bool EXACT>
-__global__ void __launch_bounds__(256) fwd_kernel(DPParams P) {
+__global__ void __launch_bounds__(320) fwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W)};
     const int w = threadIdx.x / WAVE;
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
-    if (threadIdx.x < 2 * P.W) sm.prod()[threadIdx.x] = 0;  // prod and cons are contiguous
+    if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;  // prod and cons are contiguous
     __syncthreads();
     const int t = *sm.ticket();
     const int p = t / P.G, g = t - p * P.G;
+    if (w == P.W) {  // helper wave: the previous workgroup's last row into ring 0
+        if (g > 0) helper_wave(P, sm, P.gring + ((int64_t)p * P.G + (g - 1)) * P.RW + RPAD, 0);
+        return;
+    }
     if (g * P.W + w >= P.nb) return;
     Cost cost;
     cost.init(P, p, g * P.W + w);
@@ -587,12 +601,12 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 
     // rings carry (E, R, D) of a band's first row to the band above
     float4* lring = reinterpret_cast<float4*>(sm.ring());
-    const bool in_glb = (b + 1 < nb) && (w + 1 == W);  // band below in workgroup g+1 (else LDS)
+    // LDS ring k carries the output of band k (the input of band k - 1); ring W is filled
+    // by the workgroup's helper wave from the next workgroup.
     const bool out_lds = (b > 0) && (w > 0);
     const bool out_glb = (b > 0) && (w == 0);
-    // global rows indexed by the producing group; WG g consumes what group g+1 produced
-    const float4* gin = P.gring4 + ((int64_t)p * G + (g + 1)) * M;
-    float4* gout = P.gring4 + ((int64_t)p * G + g) * M;
+    // cross-workgroup row produced by this workgroup (consumed by workgroup g - 1)
+    float4* gout = P.gring4 + ((int64_t)p * G + g) * P.RW + RPAD;
     const float4* lin = lring + (w + 1) * RS;
     float4* lout = lring + w * RS;
     const int* lin_flag = sm.prod() + (w + 1);
@@ -607,13 +621,13 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     float gD = 0.0f;
     float pE = 0.0f, pR = NINF, pD = 0.0f;  // published one step ago
 
-    float4 dn_cur[U], dn_nxt[U], hold[U];
-    float r_cur[U], r_nxt[U], d_cur[U];
+    float4 dn_cur[U], hold[U];
+    float r_cur[U], r_nxt[U], d_cur[U], d_nxt[U];
     // padding of the reference below the table and right of it (E 0, R -inf, D 0); the
     // fourth component is the row-entry tag (non-zero = written)
     const float4 pad4 = make_float4(0.0f, NINF, 0.0f, 1.0f);
-    // Band below in the same workgroup: sequence numbers [q0, q0 + U) of its first row
-    // from the LDS ring, for lane 63.
+    // Band below: sequence numbers [q0, q0 + U) of its first row from the LDS ring, for
+    // lane 63.
     auto fetch_lds = [&](int q0, float4* dst) -> bool {
 #pragma unroll
         for (int u = 0; u < U; ++u) dst[u] = pad4;
@@ -623,39 +637,6 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 #pragma unroll
         for (int u = 0; u < U; ++u) dst[u] = lin[(q0 + u) & (RS - 1)];
         if (l == 0) lds_publish(sm.cons() + (w + 1), need);
-        return true;
-    };
-    // Band below in another workgroup: lane 63 loads the row entries of sequence numbers
-    // [q0, q0 + U), one group ahead, and accepts them once none is empty.
-    auto glb_issue = [&](int q0, float4* dst) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) dst[u] = pad4;
-        if (l == WAVE - 1) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (q0 + u < M) dst[u] = glb_get4(gin + q0 + u);
-        }
-    };
-    auto glb_accept = [&](int q0, float4* v) -> bool {
-        bool miss = false;
-#pragma unroll
-        for (int u = 0; u < U; ++u) miss = miss || row_empty4(v[u]);
-        unsigned spins = 0;
-        while (__any(miss)) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > kSpinLimit) {
-                raise_timeout(P.err);
-                return false;
-            }
-            miss = false;
-            if (l == WAVE - 1) {
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    if (row_empty4(v[u])) v[u] = glb_get4(gin + q0 + u);
-                    miss = miss || row_empty4(v[u]);
-                }
-            }
-        }
         return true;
     };
     // hand the band's first row to the band above: lane 0 produced sequence numbers
@@ -670,47 +651,38 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             lds_publish(sm.prod() + w, min(max(q0 + U - (WAVE - 1), 0), M));
         } else {
 #pragma unroll
-            for (int u = 0; u < U; ++u)
-                if ((unsigned)(c0 + u) < (unsigned)M) glb_put4(gout + c0 + u, hold[u]);
+            for (int u = 0; u < U; ++u) glb_put4(gout + c0 + u, hold[u]);
         }
     };
     // forward step of reverse step q, clamped into the band (padding steps are inactive)
     auto fstep = [&](int q) { return max(M + 62 - q, 0); };
 
-    // cost tile of reverse group q0: columns [M - TC - q0, M - q0) (lane 63's newest)
+    // cost tile of reverse group q0: columns [M - TC - q0, M - q0) (lane 63's newest); the
+    // pipeline is the forward's, mirrored
     auto tile_col = [&](int q0) { return M - TC - q0; };
+    auto ring_col = [&](int q) { return ((M - 1) - q + (WAVE - 1 - l)) & (CR - 1); };
     cost.issue(tile_col(0));
-    cost.begin(tile_col(0));
+    cost.begin(cring, tile_col(0));
     cost.finish(cring, tile_col(0));
-    if (TC < S) cost.issue(tile_col(TC));
+    cost.issue(tile_col(TC));
+    cost.begin(cring, tile_col(TC));
+    cost.finish(cring, tile_col(TC));
+    cost.issue(tile_col(2 * TC));
 #pragma unroll
-    for (int u = 0; u < U; ++u) r_nxt[u] = Rt[(int64_t)fstep(u) * WAVE];
-    if (in_glb) glb_issue(0, dn_nxt);
+    for (int u = 0; u < U; ++u) {
+        r_nxt[u] = Rt[(int64_t)fstep(u) * WAVE];
+        d_nxt[u] = crow[ring_col(u)];
+    }
 
     for (int q0 = 0; q0 < S; q0 += U) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             r_cur[u] = r_nxt[u];
-            d_cur[u] = crow[((M - 1) - (q0 + u) + (WAVE - 1 - l)) & (CR - 1)];
+            d_cur[u] = d_nxt[u];
         }
-        const int t1 = q0 + TC;
-        if (t1 < S) {
-            cost.begin(tile_col(t1));
-            if (t1 + TC < S) cost.issue(tile_col(t1 + TC));
-        }
-        if (in_glb) {
-            if (!glb_accept(q0, dn_nxt)) return;
-#pragma unroll
-            for (int u = 0; u < U; ++u) dn_cur[u] = dn_nxt[u];
-        } else if (!fetch_lds(q0, dn_cur)) {
-            return;
-        }
+        cost.begin(cring, tile_col(q0 + 2 * TC));
+        if (!fetch_lds(q0, dn_cur)) return;
         const int n0 = q0 + U;
-        if (n0 < S) {
-            if (in_glb) glb_issue(n0, dn_nxt);
-#pragma unroll
-            for (int u = 0; u < U; ++u) r_nxt[u] = Rt[(int64_t)fstep(n0 + u) * WAVE];
-        }
         if (out_lds) {  // as in the forward: sequence numbers up to q0 + U - 64 this group
             const int need_free = q0 + U - WAVE + 1 - RS;
             if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err)) return;
@@ -752,23 +724,32 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             pR = mR;
             pD = mD;
             hold[u] = make_float4(mE, mR, mD, 1.0f);
+            // next group's R and costs, and the tile work, between the steps (fstep clamps
+            // reads past the band's first step)
+            r_nxt[u] = Rt[(int64_t)fstep(n0 + u) * WAVE];
+            d_nxt[u] = crow[ring_col(n0 + u)];
+            if (u == 3) cost.issue(tile_col(q0 + 3 * TC));
         }
-        if (t1 < S) cost.finish(cring, tile_col(t1));
+        cost.finish(cring, tile_col(q0 + 2 * TC));
         if (out_lds || out_glb) handover(q0);
     }
 }
 
 template <class Cost, bool BAND, bool EXACT>
-__global__ void __launch_bounds__(256) bwd_kernel(DPParams P) {
+__global__ void __launch_bounds__(320) bwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W)};
     const int w = threadIdx.x / WAVE;
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
-    if (threadIdx.x < 2 * P.W) sm.prod()[threadIdx.x] = 0;
+    if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;
     __syncthreads();
     const int t = *sm.ticket();
     const int p = t / P.G;
     const int g = (P.G - 1) - (t - p * P.G);  // lowest ticket of a pair takes the bottom group
+    if (w == P.W) {  // helper wave: the next workgroup's first row into ring W
+        if (g + 1 < P.G) helper_wave(P, sm, P.gring4 + ((int64_t)p * P.G + (g + 1)) * P.RW + RPAD, P.W);
+        return;
+    }
     if (g * P.W + w >= P.nb) return;
     Cost cost;
     cost.init(P, p, g * P.W + w);
@@ -782,7 +763,7 @@ __global__ void __launch_bounds__(256) bwd_kernel(DPParams P) {
 hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st);
 
 inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
-    const size_t ring = (size_t)P.W * RS * (bwd ? sizeof(float4) : sizeof(double));
+    const size_t ring = bwd ? ring_bytes_bwd(P.W) : ring_bytes_fwd(P.W);
     return 256 + ring + (size_t)P.W * WAVE * CS * sizeof(float);
 }
 
@@ -796,7 +777,9 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, hipStream_t st) {
     }
     hipError_t e = launch_dp_prep(P, bwd, st);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kernel, dim3(P.B * P.G), dim3(P.W * WAVE), lds, st, P);
+    // one wave per band, plus a helper wave when a pair spans several workgroups
+    const int waves = P.W + (P.G > 1 ? 1 : 0);
+    hipLaunchKernelGGL(kernel, dim3(P.B * P.G), dim3(waves * WAVE), lds, st, P);
     return hipGetLastError();
 }
 

@@ -18,8 +18,9 @@ struct DPParams {
     float* G_out;       // backward: (B,N,M) = gout * E
     const float* gout;  // backward: (B) upstream gradient or nullptr (= 1)
     int* ticket;        // workgroup ticket counter (zeroed by the prep kernel)
-    double* gring;      // forward: (B*G, M) fp64 last rows of each workgroup's bands
-    float4* gring4;     // backward: (B*G, M) (E, R, D, tag) first rows
+    double* gring;      // forward: (B*G, RW) fp64 last rows of each workgroup's bands
+    float4* gring4;     // backward: (B*G, RW) (E, R, D, tag) first rows
+    int RW;             // entries per cross-workgroup row: M plus 64 of padding each side
     int* err;           // spin-timeout flag
     int B, N, M, K;
     int nb, W, G;       // 64-row bands per pair, waves per workgroup, workgroups per pair
@@ -74,6 +75,8 @@ inline DPGeom dp_geom(int64_t N) {
 // Steps of one band in the R table: the M + 63 diagonal steps rounded up to the kernels'
 // 16-step groups (the padding steps hold +inf).
 inline int dp_band_steps(int64_t M) { return (int)(((M + 63) + 15) / 16 * 16); }
+// entries of one cross-workgroup row (M columns plus 64 entries of padding on each side)
+inline int64_t dp_row_entries(int64_t M) { return M + 128; }
 // floats in the band-skewed R table
 inline int64_t dp_table_elems(int64_t B, int64_t N, int64_t M) {
     return B * ((N + 63) / 64) * (int64_t)dp_band_steps(M) * 64;
