@@ -4,9 +4,10 @@
 //   dist_kernel       D = clamp_min(x2 + y2 - 2 x.y^T, 0): 64x64 output tiles, x/y k-slices
 //                     staged in LDS, every output's dot product a sequential FMA chain over k
 //                     (the order of the host GEMM), so D has the reference's bits.
-//   dist_bwd_kernel   gx = 2 (x * rowsum(G') - G' y) and gy = 2 (y * colsum(G') - G'^T x)
-//                     with G' = G masked by the clamp (clamp_min backward passes where
-//                     x2 + y2 - 2xy >= 0).
+//   dist_bwd_mfma_kernel
+//                     gx = 2 (x * rowsum(G') - G' y) and gy = 2 (y * colsum(G') - G'^T x)
+//                     on the matrix cores, with G' = G masked by the clamp (clamp_min
+//                     backward passes where x2 + y2 - 2xy >= 0).
 #include "sdtw_device.hpp"
 #include "sdtw_internal.hpp"
 
@@ -115,10 +116,9 @@ hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t 
 // Distance backward.  Output rows r (x rows for gx, y rows for gy), reduction index t.
 //   grad[r,k] = 2 * (W[r,k] * rs[r] - sum_t G'(r,t) Z[t,k]),   rs[r] = sum_t G'(r,t)
 // TRANS = false: gx (W = x, Z = y, G'(r,t) = G[r,t]);  TRANS = true: gy (W = y, Z = x,
-// G'(r,t) = G[t,r]).  Tile TR rows x TK features, 256 threads each owning 4 x 4 outputs.
+// G'(r,t) = G[t,r]).  G' is G with the clamp_min mask of the forward applied (cells whose
+// pre-clamp value was negative get 0).
 // ---------------------------------------------------------------------------------------
-constexpr int TT = 16;  // reduction slice
-
 template <bool MULADD>
 SDTW_DEV bool pass_mask(const DistBwdParams& p, int b, int i, int j, float d) {
     if (d > 0.0f) return true;
@@ -130,17 +130,30 @@ SDTW_DEV bool pass_mask(const DistBwdParams& p, int b, int i, int j, float d) {
     return exact_cost_pre(p.x2[(int64_t)b * p.N + i], p.y2[(int64_t)b * p.M + j], dot) >= 0.0f;
 }
 
-template <bool TRANS, int TR, int TK, bool MULADD>
-__global__ void __launch_bounds__(256) dist_bwd_kernel(DistBwdParams p) {
-    constexpr int TX = TK / 4;  // threads along k
-    static_assert((TR / 4) * TX == 256, "tile must map to 256 threads");
-    __shared__ float gs[TT][TR + 1];
-    __shared__ float zs[TT][TK + 1];
+// Matrix-core version of the same product.  A workgroup owns 64 output rows x KT features
+// (KT = 16, 32 or 64); wave w computes rows 16w..16w+15 with v_mfma_f32_16x16x4_f32, the
+// reduction index t in chunks of BT staged through double-buffered LDS by coalesced loads:
+//   gs[t][r] = G'(r0 + r, t0 + t)   (A operand: 16 rows x 4 t per instruction)
+//   zs[t][k] = Z[t0 + t][k0 + k]    (B operand: 4 t x 16 features per instruction)
+// Row sums rs[r] are accumulated from the staged G' slice.  The reduction order differs
+// from the reference's matmul; gradients are compared within rtol 1e-4 / atol 1e-5.
+constexpr int BT = 32;   // reduction chunk
+constexpr int GSS = 65;  // LDS row stride of the G' slice (floats)
+
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+template <bool TRANS, int KT, bool MULADD>
+__global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p) {
+    constexpr int KB = KT / 16;             // 16-wide feature blocks per wave
+    constexpr int GPT = 64 * BT / 256;      // G' elements loaded per thread per chunk
+    constexpr int ZPT = BT * KT / 256;      // Z elements loaded per thread per chunk
+    static_assert(ZPT >= 1 && (BT * KT) % 256 == 0, "feature tile must feed 256 threads");
+    __shared__ float gs[2][BT][GSS];
+    __shared__ float zs[2][BT][KT + 1];
     const int b = blockIdx.z;
-    const int r0 = blockIdx.y * TR;
-    const int k0 = blockIdx.x * TK;
-    const int tx = threadIdx.x % TX;
-    const int ty = threadIdx.x / TX;
+    const int r0 = blockIdx.y * 64;
+    const int k0 = blockIdx.x * KT;
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
     const int N = p.N, M = p.M, K = p.K;
     const int R_ = TRANS ? M : N;  // output rows
     const int T_ = TRANS ? N : M;  // reduction length
@@ -149,67 +162,97 @@ __global__ void __launch_bounds__(256) dist_bwd_kernel(DistBwdParams p) {
     const float* Z = TRANS ? p.x + (int64_t)b * N * K : p.y + (int64_t)b * M * K;
     const float* W = TRANS ? p.y + (int64_t)b * M * K : p.x + (int64_t)b * N * K;
     float* out = TRANS ? p.gy + (int64_t)b * M * K : p.gx + (int64_t)b * N * K;
-    float acc[4][4], rs[4];
+
+    // coalesced load of chunk t0 into registers (G' with the clamp mask applied)
+    float gv[GPT], zv[ZPT];
+    auto load_chunk = [&](int t0) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        rs[m] = 0.0f;
-#pragma unroll
-        for (int n = 0; n < 4; ++n) acc[m][n] = 0.0f;
-    }
-    for (int t0 = 0; t0 < T_; t0 += TT) {
-        // G' slice: TR rows x TT reduction entries
-        for (int e = threadIdx.x; e < TR * TT; e += 256) {
-            int r, tt;
-            if (TRANS) {  // contiguous along r in memory
-                r = e % TR;
-                tt = e / TR;
-            } else {  // contiguous along t
-                r = e / TT;
-                tt = e % TT;
+        for (int q = 0; q < GPT; ++q) {
+            const int e = tid + 256 * q;
+            int r, t;
+            if (TRANS) {  // G'(r, t) = G[t][r]: contiguous along r
+                r = e & 63;
+                t = e >> 6;
+            } else {      // G'(r, t) = G[r][t]: contiguous along t
+                r = e / BT;
+                t = e % BT;
             }
-            const int rr = r0 + r, t = t0 + tt;
+            const int rr = r0 + r, tt = t0 + t;
             float v = 0.0f;
-            if (rr < R_ && t < T_) {
-                const int i = TRANS ? t : rr;
-                const int j = TRANS ? rr : t;
+            if (rr < R_ && tt < T_) {
+                const int i = TRANS ? tt : rr;
+                const int j = TRANS ? rr : tt;
                 const int64_t idx = (int64_t)i * M + j;
                 v = Gb[idx];
                 if (p.mask && !pass_mask<MULADD>(p, b, i, j, Db[idx])) v = 0.0f;
             }
-            gs[tt][r] = v;
+            gv[q] = v;
         }
-        for (int e = threadIdx.x; e < TT * TK; e += 256) {
-            const int tt = e / TK, kk = e % TK;
-            const int t = t0 + tt, k = k0 + kk;
-            zs[tt][kk] = (t < T_ && k < K) ? Z[(int64_t)t * K + k] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < ZPT; ++q) {
+            const int e = tid + 256 * q;
+            const int t = e / KT, k = e % KT;
+            const int tt = t0 + t, kk = k0 + k;
+            zv[q] = (tt < T_ && kk < K) ? Z[(int64_t)tt * K + kk] : 0.0f;
         }
-        __syncthreads();
-#pragma unroll 4
-        for (int tt = 0; tt < TT; ++tt) {
-            float gv[4], zv[4];
+    };
+    auto store_chunk = [&](int buf) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) gv[m] = gs[tt][ty + (TR / 4) * m];
+        for (int q = 0; q < GPT; ++q) {
+            const int e = tid + 256 * q;
+            const int r = TRANS ? (e & 63) : (e / BT);
+            const int t = TRANS ? (e >> 6) : (e % BT);
+            gs[buf][t][r] = gv[q];
+        }
 #pragma unroll
-            for (int n = 0; n < 4; ++n) zv[n] = zs[tt][tx + TX * n];
+        for (int q = 0; q < ZPT; ++q) {
+            const int e = tid + 256 * q;
+            zs[buf][e / KT][e % KT] = zv[q];
+        }
+    };
+
+    floatx4_t acc[KB];
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                rs[m] += gv[m];
+    for (int kb = 0; kb < KB; ++kb) acc[kb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float rs_part = 0.0f;  // row 16w + (l & 15), t = (l >> 4) * BT/4 .. of each chunk
+
+    const int nchunks = (T_ + BT - 1) / BT;
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < nchunks) load_chunk((c + 1) * BT);  // in flight during the products
 #pragma unroll
-                for (int n = 0; n < 4; ++n) acc[m][n] = fmaf(gv[m], zv[n], acc[m][n]);
+        for (int q = 0; q < BT / 4; ++q) rs_part += gs[buf][(l >> 4) * (BT / 4) + q][16 * w + (l & 15)];
+#pragma unroll
+        for (int kk = 0; kk < BT / 4; ++kk) {
+            const float a = gs[buf][4 * kk + (l >> 4)][16 * w + (l & 15)];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const float bv = zs[buf][4 * kk + (l >> 4)][16 * kb + (l & 15)];
+                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[kb], 0, 0, 0);
             }
         }
+        if (c + 1 < nchunks) store_chunk(buf ^ 1);
         __syncthreads();
     }
+    // rs of row 16w + x: sum of the four lanes with (l & 15) == x
+    float rs = rs_part + __shfl_xor(rs_part, 16);
+    rs = rs + __shfl_xor(rs, 32);
+    // lane l holds outputs (row 16w + 4(l >> 4) + v, feature k0 + 16kb + (l & 15))
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const int r = r0 + ty + (TR / 4) * m;
+    for (int v = 0; v < 4; ++v) {
+        const int rl = 4 * (l >> 4) + v;
+        const float rsv = __shfl(rs, rl);
+        const int r = r0 + 16 * w + rl;
         if (r >= R_) continue;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-            const int k = k0 + tx + TX * n;
+        for (int kb = 0; kb < KB; ++kb) {
+            const int k = k0 + 16 * kb + (l & 15);
             if (k < K) {
                 const int64_t o = (int64_t)r * K + k;
-                out[o] = 2.0f * (W[o] * rs[m] - acc[m][n]);
+                out[o] = 2.0f * (W[o] * rsv - acc[kb][v]);
             }
         }
     }
@@ -218,13 +261,14 @@ __global__ void __launch_bounds__(256) dist_bwd_kernel(DistBwdParams p) {
 template <bool TRANS, bool MULADD>
 static void launch_dist_bwd_one(const DistBwdParams& p, hipStream_t st) {
     const int R_ = TRANS ? p.M : p.N;
-    if (p.K <= 16) {
-        dim3 grid((p.K + 15) / 16, (R_ + 255) / 256, p.B);
-        hipLaunchKernelGGL((dist_bwd_kernel<TRANS, 256, 16, MULADD>), grid, dim3(256), 0, st, p);
-    } else {
-        dim3 grid((p.K + 63) / 64, (R_ + 63) / 64, p.B);
-        hipLaunchKernelGGL((dist_bwd_kernel<TRANS, 64, 64, MULADD>), grid, dim3(256), 0, st, p);
-    }
+    const int KT = p.K <= 16 ? 16 : (p.K <= 32 ? 32 : 64);
+    dim3 grid((p.K + KT - 1) / KT, (R_ + 63) / 64, p.B);
+    if (KT == 16)
+        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 16, MULADD>), grid, dim3(256), 0, st, p);
+    else if (KT == 32)
+        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 32, MULADD>), grid, dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 64, MULADD>), grid, dim3(256), 0, st, p);
 }
 
 hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st) {
