@@ -56,6 +56,12 @@ bool gamma_ok(double gamma) { return gamma > 0.0 && isfinite(gamma); }
 // ATen's naive bmm kernel (multiply, then add) runs when K*N*M < 400.
 bool small_bmm(int64_t N, int64_t M, int64_t K) { return K * N * M < 400; }
 
+// distance-backward split-reduction scratch: partials, then counters
+size_t ws_dist_bwd(int64_t B, int64_t N, int64_t M, int64_t K) {
+    return align_up(sizeof(float) * dist_bwd_split_floats(B, N, M, K)) +
+           align_up(sizeof(int) * dist_bwd_counters(B, N, M, K));
+}
+
 size_t ws_norms(int64_t B, int64_t N, int64_t M) {
     return align_up(sizeof(float) * B * N) + align_up(sizeof(float) * B * M);
 }
@@ -184,14 +190,15 @@ size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) 
     switch (op) {
         case SDTW_OP_SQEUCLID_FWD:
         case SDTW_OP_SQEUCLID_BWD:
-            return ws_norms(B, N, M);
+            return ws_norms(B, N, M) + ws_dist_bwd(B, N, M, K);
         case SDTW_OP_FWD:
         case SDTW_OP_BWD:
             return ws_dp(B, N, M);
         case SDTW_OP_FUSED_FWD:
             return ws_norms(B, N, M) + ws_dp(B, N, M);
         case SDTW_OP_FUSED_BWD:
-            return ws_norms(B, N, M) + ws_dp(B, N, M) + align_up(sizeof(float) * B * N * M);
+            return ws_norms(B, N, M) + ws_dp(B, N, M) + align_up(sizeof(float) * B * N * M) +
+                   ws_dist_bwd(B, N, M, K);
         default:
             return 0;
     }
@@ -241,11 +248,13 @@ int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const 
     p.K = (int)K;
     p.mask = mask ? 1 : 0;
     p.muladd = small_bmm(N, M, K) ? 1 : 0;
+    Carver c{static_cast<char*>(ws), ws_bytes};
+    float* x2 = c.take<float>(B * N);
+    float* y2 = c.take<float>(B * M);
+    p.part = c.take<float>(dist_bwd_split_floats(B, N, M, K));
+    p.cnt = c.take<int>(dist_bwd_counters(B, N, M, K));
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
     if (mask) {
-        Carver c{static_cast<char*>(ws), ws_bytes};
-        float* x2 = c.take<float>(B * N);
-        float* y2 = c.take<float>(B * M);
-        if (!c.ok) return SDTW_ERR_WORKSPACE;
         hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
         if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
         if (e != hipSuccess) return SDTW_ERR_LAUNCH;
@@ -349,6 +358,8 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
     float* y2 = c.take<float>(B * M);
     const DPScratch d = carve_dp(c, B, N, M);
     float* Ebuf = c.take<float>(B * N * M);
+    float* part = c.take<float>(dist_bwd_split_floats(B, N, M, K));
+    int* cnt = c.take<int>(dist_bwd_counters(B, N, M, K));
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     int rc = fused_bwd_common(x, y, R, gout, Ebuf, x2, y2, d, B, N, M, K, gamma, bandwidth, st);
     if (rc != SDTW_OK) return rc;
@@ -367,6 +378,8 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
     q.K = (int)K;
     q.mask = 0;
     q.muladd = small_bmm(N, M, K) ? 1 : 0;
+    q.part = part;
+    q.cnt = cnt;
     return status_of(launch_dist_bwd(q, st));
 }
 

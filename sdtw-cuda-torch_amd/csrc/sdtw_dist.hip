@@ -142,15 +142,21 @@ constexpr int GSS = 65;  // LDS row stride of the G' slice (floats)
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
+// Split reduction: blockIdx.z = b * ST + st; piece st takes chunks [st*cps, (st+1)*cps).
+// With ST > 1 every piece stores W*rs - acc of its chunks as a partial (device-coherent
+// stores), waits for them to complete and counts itself in the tile's counter; the last
+// piece to arrive adds the ST partials in order 0..ST-1 (deterministic), writes the
+// gradient and resets the counter to zero for the next launch.
 template <bool TRANS, int KT, bool MULADD>
-__global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p) {
+__global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int ST) {
     constexpr int KB = KT / 16;             // 16-wide feature blocks per wave
     constexpr int GPT = 64 * BT / 256;      // G' elements loaded per thread per chunk
     constexpr int ZPT = BT * KT / 256;      // Z elements loaded per thread per chunk
     static_assert(ZPT >= 1 && (BT * KT) % 256 == 0, "feature tile must feed 256 threads");
     __shared__ float gs[2][BT][GSS];
     __shared__ float zs[2][BT][KT + 1];
-    const int b = blockIdx.z;
+    __shared__ int last_piece;
+    const int b = blockIdx.z / ST, st = blockIdx.z - b * ST;
     const int r0 = blockIdx.y * 64;
     const int k0 = blockIdx.x * KT;
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
@@ -216,13 +222,18 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p) {
     for (int kb = 0; kb < KB; ++kb) acc[kb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float rs_part = 0.0f;  // row 16w + (l & 15), t = (l >> 4) * BT/4 .. of each chunk
 
-    const int nchunks = (T_ + BT - 1) / BT;
-    load_chunk(0);
-    store_chunk(0);
+    const int total = (T_ + BT - 1) / BT;
+    const int cps = (total + ST - 1) / ST;
+    const int cbeg = min(st * cps, total), cend = min(cbeg + cps, total);
+    const int nchunks = cend - cbeg;
+    if (nchunks > 0) {
+        load_chunk(cbeg * BT);
+        store_chunk(0);
+    }
     __syncthreads();
     for (int c = 0; c < nchunks; ++c) {
         const int buf = c & 1;
-        if (c + 1 < nchunks) load_chunk((c + 1) * BT);  // in flight during the products
+        if (c + 1 < nchunks) load_chunk((cbeg + c + 1) * BT);  // in flight during the products
 #pragma unroll
         for (int q = 0; q < BT / 4; ++q) rs_part += gs[buf][(l >> 4) * (BT / 4) + q][16 * w + (l & 15)];
 #pragma unroll
@@ -241,37 +252,84 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p) {
     float rs = rs_part + __shfl_xor(rs_part, 16);
     rs = rs + __shfl_xor(rs, 32);
     // lane l holds outputs (row 16w + 4(l >> 4) + v, feature k0 + 16kb + (l & 15))
+    float val[4][KB];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int rl = 4 * (l >> 4) + v;
         const float rsv = __shfl(rs, rl);
-        const int r = r0 + 16 * w + rl;
+        const int r = min(r0 + 16 * w + rl, R_ - 1);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            const int k = min(k0 + 16 * kb + (l & 15), K - 1);
+            val[v][kb] = W[(int64_t)r * K + k] * rsv - acc[kb][v];
+        }
+    }
+    if (ST > 1) {
+        const int64_t tile = ((int64_t)b * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        float* part = p.part + tile * ST * 64 * KT;
+        // partial of piece st: element (row 16w + 4(l>>4) + v, feature 16kb + (l&15))
+        auto pidx = [&](int q, int v, int kb) {
+            return ((int64_t)q * 64 + 16 * w + 4 * (l >> 4) + v) * KT + 16 * kb + (l & 15);
+        };
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+                __hip_atomic_store(part + pidx(st, v, kb), val[v][kb], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this thread's partials are stored
+        __syncthreads();
+        if (tid == 0)
+            last_piece = __hip_atomic_fetch_add(p.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ST - 1;
+        __syncthreads();
+        if (!last_piece) return;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                float sum = 0.0f;
+                for (int q = 0; q < ST; ++q)
+                    sum += __hip_atomic_load(part + pidx(q, v, kb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                val[v][kb] = sum;
+            }
+        if (tid == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int r = r0 + 16 * w + 4 * (l >> 4) + v;
         if (r >= R_) continue;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
             const int k = k0 + 16 * kb + (l & 15);
-            if (k < K) {
-                const int64_t o = (int64_t)r * K + k;
-                out[o] = 2.0f * (W[o] * rsv - acc[kb][v]);
-            }
+            if (k < K) out[(int64_t)r * K + k] = 2.0f * val[v][kb];
         }
     }
 }
 
+__global__ void zero_ints_kernel(int* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
 template <bool TRANS, bool MULADD>
 static void launch_dist_bwd_one(const DistBwdParams& p, hipStream_t st) {
-    const int R_ = TRANS ? p.M : p.N;
-    const int KT = p.K <= 16 ? 16 : (p.K <= 32 ? 32 : 64);
-    dim3 grid((p.K + KT - 1) / KT, (R_ + 63) / 64, p.B);
+    const int R_ = TRANS ? p.M : p.N, T_ = TRANS ? p.N : p.M;
+    const int KT = dist_bwd_kt(p.K);
+    const int ST = p.part ? dist_bwd_splits(p.B, R_, T_, p.K) : 1;
+    dim3 grid((p.K + KT - 1) / KT, (R_ + 63) / 64, p.B * ST);
     if (KT == 16)
-        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 16, MULADD>), grid, dim3(256), 0, st, p);
+        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 16, MULADD>), grid, dim3(256), 0, st, p, ST);
     else if (KT == 32)
-        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 32, MULADD>), grid, dim3(256), 0, st, p);
+        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 32, MULADD>), grid, dim3(256), 0, st, p, ST);
     else
-        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 64, MULADD>), grid, dim3(256), 0, st, p);
+        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 64, MULADD>), grid, dim3(256), 0, st, p, ST);
 }
 
 hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st) {
+    if (p.part) {  // counters start at zero; every pass leaves them at zero
+        const int64_t n = dist_bwd_counters(p.B, p.N, p.M, p.K);
+        const int blocks = (int)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
+        hipLaunchKernelGGL(zero_ints_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, st, p.cnt, n);
+    }
     if (p.muladd) {
         launch_dist_bwd_one<false, true>(p, st);
         launch_dist_bwd_one<true, true>(p, st);

@@ -49,7 +49,35 @@ struct DistBwdParams {
     int B, N, M, K;
     int mask;
     int muladd;
+    float* part;      // split-reduction partials (dist_bwd_split_floats) or nullptr
+    int* cnt;         // per-tile arrival counters (dist_bwd_tiles ints), or nullptr
 };
+
+// Split reduction of the distance backward: the reduction of a 64-row x KT-feature output
+// tile is cut into dist_bwd_splits() pieces so that about 1024 workgroups are in flight.
+inline int dist_bwd_kt(int64_t K) { return K <= 16 ? 16 : (K <= 32 ? 32 : 64); }
+inline int64_t dist_bwd_tiles(int64_t B, int64_t R, int64_t K) {
+    return B * ((R + 63) / 64) * ((K + dist_bwd_kt(K) - 1) / dist_bwd_kt(K));
+}
+inline int dist_bwd_splits(int64_t B, int64_t R, int64_t T, int64_t K) {
+    const int64_t tiles = dist_bwd_tiles(B, R, K);
+    const int64_t chunks = (T + 31) / 32;
+    int64_t st = (1024 + tiles - 1) / tiles;
+    st = st > 8 ? 8 : st;
+    st = st > chunks ? chunks : st;
+    return (int)(st < 1 ? 1 : st);
+}
+// scratch floats / counters for both passes (gx over N rows, gy over M rows), reused
+inline int64_t dist_bwd_split_floats(int64_t B, int64_t N, int64_t M, int64_t K) {
+    const int64_t kt = dist_bwd_kt(K);
+    const int64_t a = dist_bwd_tiles(B, N, K) * dist_bwd_splits(B, N, M, K);
+    const int64_t b = dist_bwd_tiles(B, M, K) * dist_bwd_splits(B, M, N, K);
+    return (a > b ? a : b) * 64 * kt;
+}
+inline int64_t dist_bwd_counters(int64_t B, int64_t N, int64_t M, int64_t K) {
+    const int64_t a = dist_bwd_tiles(B, N, K), b = dist_bwd_tiles(B, M, K);
+    return a > b ? a : b;
+}
 
 hipError_t launch_norms(const float* v, float* out, int64_t rows, int K, hipStream_t st);
 hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t st);
