@@ -1,6 +1,6 @@
 // sdtw_dist.hip -- squared-Euclidean cost and its gradient for gfx950.
 //
-//   norms_kernel      x2[r] = sum_k x[r,k]^2 in ATen's CPU order (one lane per row).
+//   norms_kernel      x2[r] = sum_k x[r,k]^2 in ATen's CPU order (eight lanes per row).
 //   dist_kernel       D = clamp_min(x2 + y2 - 2 x.y^T, 0): 64x64 output tiles, x/y k-slices
 //                     staged in LDS, every output's dot product a sequential FMA chain over k
 //                     (the order of the host GEMM), so D has the reference's bits.
@@ -13,16 +13,39 @@
 
 namespace sdtw {
 
+// Eight threads per row: for K >= 8 thread t computes ATen's vector lane t (the scalar
+// row_sum over v[8c + t]); the row's first thread adds the tail and the eight lane sums in
+// ATen's order (aten_sumsq), so the result has the same bits with 8x the parallelism.
 __global__ void __launch_bounds__(256) norms_kernel(const float* __restrict__ v,
                                                     float* __restrict__ out, int64_t rows,
                                                     int K) {
-    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (r < rows) out[r] = aten_sumsq(v + r * K, K);
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t r = gid >> 3;
+    const int t = (int)(gid & 7);
+    const bool ok = r < rows;
+    const float* row = v + (ok ? r : 0) * K;
+    if (K >= 8) {
+        const int nvec = K / 8;
+        const float part = ok ? aten_row_sum_sq(row + t, 8, nvec) : 0.0f;
+        const int base = (int)(threadIdx.x & 63) & ~7;
+        float lane[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) lane[j] = __shfl(part, base + j);
+        if (ok && t == 0) {
+            float fa = 0.0f;
+            for (int e = nvec * 8; e < K; ++e) fa = __fadd_rn(fa, sq(row[e]));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) fa = __fadd_rn(fa, lane[j]);
+            out[r] = fa;
+        }
+    } else if (ok && t == 0) {
+        out[r] = __fadd_rn(0.0f, aten_row_sum_sq(row, 1, K));
+    }
 }
 
 hipError_t launch_norms(const float* v, float* out, int64_t rows, int K, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
-    const int64_t blocks = (rows + 255) / 256;
+    const int64_t blocks = (rows * 8 + 255) / 256;
     hipLaunchKernelGGL(norms_kernel, dim3((unsigned)blocks), dim3(256), 0, st, v, out, rows,
                        K);
     return hipGetLastError();

@@ -198,14 +198,12 @@ SDTW_DEV float bwd_cell_hw(float rij, float En, float Rn, float Dn, float Er, fl
 // conflict-free ds_read (CS - 1 is odd).  The live window of a group is 64 + 2*TC columns,
 // inside CR.  Ring slots of columns outside [0, M) hold values that are never used.
 //
-// Provider interface (all lanes call each function, wave-uniform arguments), for the tile
-// at columns [c0, c0 + TC):
-//   issue(c0)        start its memory loads
-//   begin(ring, c0)  use the loaded operands: write the tile (loads) or start its
-//                    arithmetic (matrix cores, which run while the wave goes on with the
-//                    recursion); the next issue() may then reuse the operand registers
-//   finish(ring, c0) complete it in the ring (matrix cores; no-op otherwise)
-// Per group: begin(t), issue(t + TC) a few steps later, ...recursion..., finish(t).
+// Provider interface (all lanes call each function, wave-uniform arguments).  Per group,
+// with c the tile completed this group and cn the tile after it:
+//   begin(ring, c)     at the group start
+//   step(u, cn)        inside recursion step u (matrix-core products, loads), u = 0..U-1
+//   end(ring, c, cn)   after the last step; tile c is in the ring afterwards
+// prologue(ring, c) stages tile c synchronously; preload(c) starts the first pipelined one.
 // ---------------------------------------------------------------------------------------
 constexpr int CR = 128;  // ring columns (power of two)
 constexpr int CS = 144;  // row stride in floats: CS mod 64 = 16 (tile writes by 4-row
@@ -234,13 +232,25 @@ struct CostD {
             v[k] = base[(int64_t)row * M + col];
         }
     }
-    SDTW_DEV void begin(float* ring, int c0) {
+    // write the loaded tile c0 into the ring
+    SDTW_DEV void store(float* ring, int c0) {
         const int l = threadIdx.x & (WAVE - 1);
         float* dst = ring + (l >> 4) * CS + ((c0 + (l & 15)) & (CR - 1));
 #pragma unroll
         for (int k = 0; k < 16; ++k) dst[4 * k * CS] = v[k];
     }
-    SDTW_DEV void finish(float*, int) {}
+    SDTW_DEV void prologue(float* ring, int c) {
+        issue(c);
+        store(ring, c);
+    }
+    SDTW_DEV void preload(int c) { issue(c); }
+    // the tile loaded during the previous group lands at the group start; the next one is
+    // loaded from step 3 on, a whole group ahead of its use
+    SDTW_DEV void begin(float* ring, int c) { store(ring, c); }
+    SDTW_DEV void step(int u, int cn) {
+        if (u == 3) issue(cn);
+    }
+    SDTW_DEV void end(float*, int, int) {}
 };
 
 // Fused: cost = max(0, (|x_i|^2 + |y_j|^2) - 2 x_i.y_j) with the dot on the matrix cores.
@@ -293,15 +303,38 @@ struct CostMfma {
         }
         y2n = y2[col];
     }
-    SDTW_DEV void begin(float*, int) {
+    // k-step kk of the tile's products (four independent accumulation chains)
+    SDTW_DEV void mma(int kk) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+            acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[rb][kk], yb[kk], acc[rb], 0, 0, 0);
+    }
+    SDTW_DEV void zero() {
         y2c = y2n;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) acc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    SDTW_DEV void prologue(float* ring, int c) {
+        issue(c);
+        zero();
 #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk)
+        for (int kk = 0; kk < NKK; ++kk) mma(kk);
+        finish(ring, c);
+    }
+    SDTW_DEV void preload(int c) { issue(c); }
+    // one k-step per recursion step, so the matrix pipe never holds up the wave's in-order
+    // issue; the next tile's B operand is loaded after the last product has read it
+    SDTW_DEV void begin(float*, int) { zero(); }
+    SDTW_DEV void step(int u, int) {
+        if (u < NKK) mma(u);
+    }
+    SDTW_DEV void end(float* ring, int c, int cn) {
+        if (U < NKK) {  // more k-steps than recursion steps
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-                acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[rb][kk], yb[kk], acc[rb], 0, 0, 0);
+            for (int kk = U; kk < NKK; ++kk) mma(kk);
+        }
+        finish(ring, c);
+        issue(cn);
     }
     SDTW_DEV void finish(float* ring, int c0) {
         const int l = threadIdx.x & (WAVE - 1);
@@ -334,8 +367,11 @@ struct CostScalar {
         x2 = P.x2 + (int64_t)p * N;
         y2 = P.y2 + (int64_t)p * M;
     }
-    SDTW_DEV void issue(int) {}
+    SDTW_DEV void prologue(float* ring, int c) { finish(ring, c); }
+    SDTW_DEV void preload(int) {}
     SDTW_DEV void begin(float*, int) {}
+    SDTW_DEV void step(int, int) {}
+    SDTW_DEV void end(float* ring, int c, int) { finish(ring, c); }
     SDTW_DEV void finish(float* ring, int c0) {
         const int l = threadIdx.x & (WAVE - 1);
         const int col = min(max(c0 + (l & 15), 0), M - 1);
@@ -452,13 +488,9 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     //     (finish, after the last step), so the ring holds tiles up to s0 + 2*TC;
     //   - the band above's row is read from the LDS ring at the group start.
     // Tiles past the table are harmless: loads are clamped and their slots are not live.
-    cost.issue(0);
-    cost.begin(cring, 0);
-    cost.finish(cring, 0);
-    cost.issue(TC);
-    cost.begin(cring, TC);
-    cost.finish(cring, TC);
-    cost.issue(2 * TC);
+    cost.prologue(cring, 0);
+    cost.prologue(cring, TC);
+    cost.preload(2 * TC);
 #pragma unroll
     for (int u = 0; u < U; ++u) d_nxt[u] = crow[(u - l) & (CR - 1)];
 
@@ -499,9 +531,9 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             Rg[u * WAVE] = (float)r;
             // next group's costs, and the tile work, between the steps
             d_nxt[u] = crow[(s0 + TC + u - l) & (CR - 1)];
-            if (u == 3) cost.issue(s0 + 3 * TC);
+            cost.step(u, s0 + 3 * TC);
         }
-        cost.finish(cring, s0 + 2 * TC);
+        cost.end(cring, s0 + 2 * TC, s0 + 3 * TC);
         if (out_lds || out_glb) handover(s0);
     }
     // out[p] = R[N-1, M-1] as stored (step M-1+l of this lane, written by this lane)
@@ -661,13 +693,9 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // pipeline is the forward's, mirrored
     auto tile_col = [&](int q0) { return M - TC - q0; };
     auto ring_col = [&](int q) { return ((M - 1) - q + (WAVE - 1 - l)) & (CR - 1); };
-    cost.issue(tile_col(0));
-    cost.begin(cring, tile_col(0));
-    cost.finish(cring, tile_col(0));
-    cost.issue(tile_col(TC));
-    cost.begin(cring, tile_col(TC));
-    cost.finish(cring, tile_col(TC));
-    cost.issue(tile_col(2 * TC));
+    cost.prologue(cring, tile_col(0));
+    cost.prologue(cring, tile_col(TC));
+    cost.preload(tile_col(2 * TC));
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         r_nxt[u] = Rt[(int64_t)fstep(u) * WAVE];
@@ -728,9 +756,9 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             // reads past the band's first step)
             r_nxt[u] = Rt[(int64_t)fstep(n0 + u) * WAVE];
             d_nxt[u] = crow[ring_col(n0 + u)];
-            if (u == 3) cost.issue(tile_col(q0 + 3 * TC));
+            cost.step(u, tile_col(q0 + 3 * TC));
         }
-        cost.finish(cring, tile_col(q0 + 2 * TC));
+        cost.end(cring, tile_col(q0 + 2 * TC), tile_col(q0 + 3 * TC));
         if (out_lds || out_glb) handover(q0);
     }
 }
