@@ -59,11 +59,13 @@ SDTW_DEV double shr1(double old, double v) {
     return __hiloint2double(hi, lo);
 }
 
-// LDS flags: relaxed accesses; LDS operations of a wave complete in order, and the explicit
-// lgkmcnt wait before a publish makes the ring data visible first.
+// LDS counters: relaxed accesses.  All LDS operations of a CU are performed as wave-wide
+// operations in one global order, a wave's in issue order, so a counter stored after ring
+// writes (or after ring reads) is seen by another wave only after those are performed.  The
+// compiler fence keeps the program order; no wait on the hardware counters is needed.
 SDTW_DEV int lds_load(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 SDTW_DEV void lds_publish(int* p, int v) {
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): prior LDS writes done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 // Cross-workgroup rows.  Every access is an agent-scope (device-coherent, sc1) atomic, so
@@ -201,7 +203,7 @@ SDTW_DEV float bwd_cell_hw(float rij, float En, float Rn, float Dn, float Er, fl
 // Provider interface (all lanes call each function, wave-uniform arguments).  Per group,
 // with c the tile completed this group and cn the tile after it:
 //   begin(ring, c)     at the group start
-//   step(u, cn)        inside recursion step u (matrix-core products, loads), u = 0..U-1
+//   step(u, c, cn)     inside recursion step u (matrix-core products, loads), u = 0..U-1
 //   end(ring, c, cn)   after the last step; tile c is in the ring afterwards
 // prologue(ring, c) stages tile c synchronously; preload(c) starts the first pipelined one.
 // ---------------------------------------------------------------------------------------
@@ -243,14 +245,13 @@ struct CostD {
         issue(c);
         store(ring, c);
     }
-    SDTW_DEV void preload(int c) { issue(c); }
-    // the tile loaded during the previous group lands at the group start; the next one is
-    // loaded from step 3 on, a whole group ahead of its use
-    SDTW_DEV void begin(float* ring, int c) { store(ring, c); }
-    SDTW_DEV void step(int u, int cn) {
-        if (u == 3) issue(cn);
+    SDTW_DEV void preload(int) {}
+    // the tile is loaded at the first step and lands in the ring after the last one
+    SDTW_DEV void begin(float*, int) {}
+    SDTW_DEV void step(int u, int c, int) {
+        if (u == 0) issue(c);
     }
-    SDTW_DEV void end(float*, int, int) {}
+    SDTW_DEV void end(float* ring, int c, int) { store(ring, c); }
 };
 
 // Fused: cost = max(0, (|x_i|^2 + |y_j|^2) - 2 x_i.y_j) with the dot on the matrix cores.
@@ -325,7 +326,7 @@ struct CostMfma {
     // one k-step per recursion step, so the matrix pipe never holds up the wave's in-order
     // issue; the next tile's B operand is loaded after the last product has read it
     SDTW_DEV void begin(float*, int) { zero(); }
-    SDTW_DEV void step(int u, int) {
+    SDTW_DEV void step(int u, int, int) {
         if (u < NKK) mma(u);
     }
     SDTW_DEV void end(float* ring, int c, int cn) {
@@ -370,7 +371,7 @@ struct CostScalar {
     SDTW_DEV void prologue(float* ring, int c) { finish(ring, c); }
     SDTW_DEV void preload(int) {}
     SDTW_DEV void begin(float*, int) {}
-    SDTW_DEV void step(int, int) {}
+    SDTW_DEV void step(int, int, int) {}
     SDTW_DEV void end(float* ring, int c, int) { finish(ring, c); }
     SDTW_DEV void finish(float* ring, int c0) {
         const int l = threadIdx.x & (WAVE - 1);
@@ -486,7 +487,8 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     //   - the tile two groups ahead takes its operands (begin), the one three groups ahead
     //     starts loading (issue, after step 3), and the tile two ahead lands in the ring
     //     (finish, after the last step), so the ring holds tiles up to s0 + 2*TC;
-    //   - the band above's row is read from the LDS ring at the group start.
+    //   - the band above's row is read from the LDS ring at the group start (reading it
+    //     a group ahead would add a group of lag per band boundary).
     // Tiles past the table are harmless: loads are clamped and their slots are not live.
     cost.prologue(cring, 0);
     cost.prologue(cring, TC);
@@ -531,7 +533,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             Rg[u * WAVE] = (float)r;
             // next group's costs, and the tile work, between the steps
             d_nxt[u] = crow[(s0 + TC + u - l) & (CR - 1)];
-            cost.step(u, s0 + 3 * TC);
+            cost.step(u, s0 + 2 * TC, s0 + 3 * TC);
         }
         cost.end(cring, s0 + 2 * TC, s0 + 3 * TC);
         if (out_lds || out_glb) handover(s0);
@@ -756,7 +758,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             // reads past the band's first step)
             r_nxt[u] = Rt[(int64_t)fstep(n0 + u) * WAVE];
             d_nxt[u] = crow[ring_col(n0 + u)];
-            cost.step(u, tile_col(q0 + 3 * TC));
+            cost.step(u, tile_col(q0 + 2 * TC), tile_col(q0 + 3 * TC));
         }
         cost.end(cring, tile_col(q0 + 2 * TC), tile_col(q0 + 3 * TC));
         if (out_lds || out_glb) handover(q0);
