@@ -129,35 +129,42 @@ SDTW_DEV void raise_timeout(int* err) { __hip_atomic_store(err, 1, __ATOMIC_RELA
 // Soft-min of the three predecessors (diag R0, up R1, left R2) in fp64: the reference CPU
 // formula (launcher.py:317-322) restated around the minimum m as
 //   m - gamma * log(sum_k exp(-(R_k - m) / gamma)),
-// summed in the reference's index order ((t0 + t1) + t2; the minimum's term is exactly 1).
-// The value path has no compare-and-select: the minimum is a min instruction and the
-// exponential's lower clamp a max.  Those drop NaN operands, so NaN is put back
-// explicitly: `nanfix` is NaN when an input is NaN or all three are +inf (where the
-// reference's expression evaluates inf - inf), else 0.
+// summed in the reference's index order ((t0 + t1) + t2).  The minimum's term is exactly 1,
+// so only the other two exponentials are evaluated; with the first minimum at index a,
+//   a = 0 or 1: (1 + e_first) + e_second,   a = 2: (e_first + e_second) + 1,
+// the same sums as the reference's.  exp / log are the table-driven fp64 ones (T, L in
+// LDS).  Min and maxNum drop NaN operands, so NaN is put back explicitly: `nanfix` is NaN
+// when an input is NaN or all three are +inf (where the reference's expression evaluates
+// inf - inf), else 0.
 SDTW_DEV double softmin_exact(double R0, double R1, double R2, double gamma, double inv_gamma,
-                             double& nanfix) {
+                              double& nanfix, const double* T, const double* L) {
     const double m = fmin(fmin(R0, R1), R2);
     const bool nan_in = (R0 != R0) || (R1 != R1) || (R2 != R2);
     nanfix = (m - m) + (nan_in ? __builtin_nan("") : 0.0);
-    const double e0 = fm::exp_neg<10>((m - R0) * inv_gamma);
-    const double e1 = fm::exp_neg<10>((m - R1) * inv_gamma);
-    const double e2 = fm::exp_neg<10>((m - R2) * inv_gamma);
-    const double rsum = (e0 + e1) + e2;
-    return fma(-gamma, fm::log_1to3(rsum), m);
+    const bool a0 = (R0 == m);
+    const bool a2 = !a0 && !(R1 == m);
+    const double Ra = a0 ? R1 : R0;  // the two other predecessors, in index order
+    const double Rb = a2 ? R1 : R2;
+    const double ea = fm::exp_tab((m - Ra) * inv_gamma, T);
+    const double eb = fm::exp_tab((m - Rb) * inv_gamma, T);
+    const double p = a2 ? eb : 1.0, q = a2 ? 1.0 : eb;
+    const double rsum = (ea + p) + q;
+    return fma(-gamma, fm::log_tab_1to3(rsum, L), m);
 }
 
 // One backward cell (launcher.py:347-351): fp32 differences, fp64 exp/products/sum (in the
 // reference's order), E rounded to fp32.  The exponential's clamp drops NaN, which is put
 // back explicitly.
 SDTW_DEV float bwd_cell_exact(float rij, float En, float Rn, float Dn, float Er, float Rr,
-                             float Dr, float Eg, float Rg, float Dg, double inv_gamma) {
+                              float Dr, float Eg, float Rg, float Dg, double inv_gamma,
+                              const double* T) {
     const float da = __fsub_rn(__fsub_rn(Rn, rij), Dn);
     const float db = __fsub_rn(__fsub_rn(Rr, rij), Dr);
     const float dc = __fsub_rn(__fsub_rn(Rg, rij), Dg);
     const bool nan_in = (da != da) || (db != db) || (dc != dc);
-    const double a = fm::exp_neg<9>((double)da * inv_gamma);
-    const double b = fm::exp_neg<9>((double)db * inv_gamma);
-    const double c = fm::exp_neg<9>((double)dc * inv_gamma);
+    const double a = fm::exp_tab((double)da * inv_gamma, T);
+    const double b = fm::exp_tab((double)db * inv_gamma, T);
+    const double c = fm::exp_tab((double)dc * inv_gamma, T);
     double acc = __dmul_rn((double)En, a);
     acc = __dadd_rn(acc, __dmul_rn((double)Er, b));
     acc = __dadd_rn(acc, __dmul_rn((double)Eg, c));
@@ -389,8 +396,10 @@ struct CostScalar {
     }
 };
 
-// shared-memory layout of the DP kernels: [ticket, counters][handoff rings][cost rings];
+// shared-memory layout of the DP kernels:
+//   [ticket, counters 256 B][exp / log tables 1536 B][handoff rings][cost rings]
 // W + 1 produced/consumed counter pairs, one per handoff ring
+constexpr int kTabBytes = (64 + 128) * 8;
 struct Smem {
     unsigned char* base;
     int W;
@@ -398,9 +407,16 @@ struct Smem {
     SDTW_DEV int* ticket() const { return reinterpret_cast<int*>(base); }
     SDTW_DEV int* prod() const { return reinterpret_cast<int*>(base) + 4; }
     SDTW_DEV int* cons() const { return reinterpret_cast<int*>(base) + 4 + (W + 1); }
-    SDTW_DEV unsigned char* ring() const { return base + 256; }
+    SDTW_DEV double* tables() const { return reinterpret_cast<double*>(base + 256); }
+    SDTW_DEV unsigned char* ring() const { return base + 256 + kTabBytes; }
     SDTW_DEV float* cost_ring(int w) const {
-        return reinterpret_cast<float*>(base + 256 + ring_bytes) + (size_t)w * WAVE * CS;
+        return reinterpret_cast<float*>(base + 256 + kTabBytes + ring_bytes) + (size_t)w * WAVE * CS;
+    }
+    // every thread of the workgroup, before the first barrier
+    SDTW_DEV void load_tables() const {
+        double* t = tables();
+        for (int e = threadIdx.x; e < 64 + 128; e += blockDim.x)
+            t[e] = e < 64 ? fm::kExp2Tab[e] : fm::kLogTab[e - 64];
     }
 };
 
@@ -424,6 +440,8 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const double INF = dinf();
 
     double* lring = reinterpret_cast<double*>(sm.ring());
+    const double* tabE = sm.tables();     // exp / log tables in LDS
+    const double* tabL = tabE + 64;
     float* cring = sm.cost_ring(w);
     const float* crow = cring + l * CS;  // my row of the cost ring
     // LDS ring k carries the input of band k of this workgroup: ring 0 is filled by the
@@ -518,7 +536,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             double cand;
             if (EXACT) {
                 double nanfix;
-                const double sm_ = softmin_exact(diag, up, left, gamma, inv_gamma, nanfix);
+                const double sm_ = softmin_exact(diag, up, left, gamma, inv_gamma, nanfix, tabE, tabL);
                 cand = ((double)d_cur[u] + sm_) + nanfix;
             } else {
                 cand = fwd_cell_hw(diag, up, left, d_cur[u], c2, ngl);
@@ -590,6 +608,7 @@ __global__ void __launch_bounds__(320) fwd_kernel(DPParams P) {
     const int w = threadIdx.x / WAVE;
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;  // prod and cons are contiguous
+    sm.load_tables();
     __syncthreads();
     const int t = *sm.ticket();
     const int p = t / P.G, g = t - p * P.G;
@@ -626,6 +645,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const float c2 = (float)(inv_gamma * 1.4426950408889634074);  // log2(e) / gamma
     const float NINF = -finf();
     const float gsc = P.gout ? P.gout[p] : 1.0f;
+    const double* tabE = sm.tables();  // exp table in LDS
     float* cring = sm.cost_ring(w);
     const float* crow = cring + l * CS;  // my row of the cost ring
 
@@ -733,7 +753,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             const bool act = row_ok && (unsigned)j < (unsigned)M;
             float rij = r_cur[u];
             rij = __builtin_isinf(rij) ? NINF : rij;
-            const float cand = EXACT ? bwd_cell_exact(rij, dE, dR, dD, rE, rR, rD, gE, gR, gD, inv_gamma)
+            const float cand = EXACT ? bwd_cell_exact(rij, dE, dR, dD, rE, rR, rD, gE, gR, gD, inv_gamma, tabE)
                                      : bwd_cell_hw(rij, dE, dR, dD, rE, rR, rD, gE, gR, gD, c2);
             bool keep = true;
             if (BAND) keep = !out_of_band(bw, i, j);
@@ -772,6 +792,7 @@ __global__ void __launch_bounds__(320) bwd_kernel(DPParams P) {
     const int w = threadIdx.x / WAVE;
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;
+    sm.load_tables();
     __syncthreads();
     const int t = *sm.ticket();
     const int p = t / P.G;
@@ -794,7 +815,7 @@ hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st);
 
 inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
     const size_t ring = bwd ? ring_bytes_bwd(P.W) : ring_bytes_fwd(P.W);
-    return 256 + ring + (size_t)P.W * WAVE * CS * sizeof(float);
+    return 256 + kTabBytes + ring + (size_t)P.W * WAVE * CS * sizeof(float);
 }
 
 template <class K>
