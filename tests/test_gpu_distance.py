@@ -39,7 +39,11 @@ def test_distance_clamp_and_self():
 
 
 @pytest.mark.parametrize("B,N,M,K,selfpair", [(2, 30, 20, 5, False), (3, 64, 64, 8, True),
-                                              (2, 128, 96, 64, False)])
+                                              (2, 128, 96, 64, False),
+                                              # split reduction (several pieces per tile),
+                                              # padded and multi-tile feature widths
+                                              (4, 300, 500, 33, False), (2, 70, 90, 100, False),
+                                              (1, 1000, 40, 1, False)])
 def test_distance_backward_matches_torch_autograd(B, N, M, K, selfpair):
     say(f"[dist bwd] B={B} N={N} M={M} K={K} self={selfpair}")
     x, y = randn_pair(B, N, M, K, seed=11)

@@ -137,6 +137,23 @@ def test_backward_scales_by_grad_output():
     torch.testing.assert_close(G, g.view(-1, 1, 1) * E, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("K", [1, 33, 100])
+def test_fused_feature_widths_match_unfused(K):
+    # K = 1: matrix-core tiles padded from 1 to 4 features; K = 33: padded to 64; K = 100:
+    # the scalar tile fallback beyond the register-resident width
+    B, N, M = 2, 150, 90
+    x, y = randn_pair(B, N, M, K, seed=K)
+    xg, yg = x.cuda(), y.cuda()
+    D = _engine.sqeuclid_fwd(xg, yg)
+    assert torch.equal(D.cpu(), oracle.sqeuclidean(x, y))
+    o1, R1 = _engine.dtw_fwd(D, 0.5, -1.0)
+    o2, R2 = _engine.fused_fwd(xg, yg, 0.5, -1.0)
+    assert torch.equal(o1, o2) and torch.equal(R1, R2)
+    E1 = _engine.dtw_bwd(D, R1, 0.5, -1.0)
+    E2 = _engine.fused_bwd_e(xg, yg, R2, 0.5, -1.0)
+    assert torch.equal(E1, E2)
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_fused_matches_unfused_kernels(mode):
     # fused recomputes the same cost bits: identical out / R / E
