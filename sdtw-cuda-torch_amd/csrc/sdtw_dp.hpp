@@ -28,7 +28,7 @@
 //     what the backward reads back.
 //   * Two cell arithmetics (template flag EXACT):
 //       - exact (default): the reference CPU arithmetic restated with fp64-accurate exp / log
-//         written out as polynomials; R rounds to the CPU path's fp32 bits;
+//         (table-driven, tables staged in LDS); R rounds to the CPU path's fp32 bits;
 //       - fast: the same fp64 state, but the soft-min's correction term and the backward's
 //         transition weights use the hardware fp32 exp2 / log2.  The correction is at most
 //         gamma*log(3) per cell, so R stays within ~1 fp32 ulp of the exact recursion.
