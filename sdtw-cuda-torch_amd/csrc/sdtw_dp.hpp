@@ -647,7 +647,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const float gsc = P.gout ? P.gout[p] : 1.0f;
     const double* tabE = sm.tables();  // exp table in LDS
     float* cring = sm.cost_ring(w);
-    const float* crow = cring + l * CS;  // my row of the cost ring
+    float* crow = cring + l * CS;  // my row of the cost ring
 
     // corner R (as stored by the forward) of this pair
     const int lb = nb - 1, ll = (N - 1) - lb * WAVE;
@@ -666,7 +666,9 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const int* lin_flag = sm.prod() + (w + 1);
 
     const float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
-    float* Grow = P.G_out + ((int64_t)p * N + (row_ok ? i : N - 1)) * M;
+    // G tile stores: lane l covers column (l & 15) of rows 4k + (l >> 4) of the band
+    const int nrows = min(N - b * WAVE, WAVE);
+    float* Gband = P.G_out + ((int64_t)p * N + b * WAVE + (l >> 4)) * M + (l & 15);
 
     int known_in = 0, known_free = 0;
     float rE = 0.0f, rR = NINF, rD = 0.0f;  // right neighbour
@@ -706,6 +708,37 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         } else {
 #pragma unroll
             for (int u = 0; u < U; ++u) glb_put4(gout + c0 + u, hold[u]);
+        }
+    };
+    // Each step writes g*E of the lane's cell into the cost-ring slot whose cost it has just
+    // consumed (its own row, column j), whether or not the cell is in the table.  The group
+    // at q0 completes columns [M + 47 - q0, M + 63 - q0) of every row (lane 0 visits column
+    // M + 62 - q), which are stored here as 16 coalesced tile rows.  No slot is reused while
+    // still live: at the end of group q0 the ring holds columns from the newest cost tile,
+    // M - 48 - q0, up to M + 62 - q0, 111 < CR columns; writes of cells outside the table
+    // land on slots of columns that are rewritten before use or already stored.
+    auto flush = [&](int q0) {
+        const int c0 = M + 47 - q0;
+        if (c0 >= M || c0 + TC <= 0) return;
+        const int col = c0 + (l & 15);
+        if ((unsigned)col >= (unsigned)M) return;
+        const float* src = cring + (l >> 4) * CS + (col & (CR - 1));
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = src[4 * k * CS];
+        float* dst = Gband + c0;
+        if (nrows == WAVE) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                *dst = v[k];
+                dst += 4 * M;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                if (4 * k + (l >> 4) < nrows) *dst = v[k];
+                dst += 4 * M;
+            }
         }
     };
     // forward step of reverse step q, clamped into the band (padding steps are inactive)
@@ -758,7 +791,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             bool keep = true;
             if (BAND) keep = !out_of_band(bw, i, j);
             const float e = keep ? cand : 0.0f;
-            if (act) Grow[j] = __fmul_rn(gsc, e);
+            crow[j & (CR - 1)] = __fmul_rn(gsc, e);
             // inactive steps carry the reference's padding (E 0, R -inf, D 0): before a
             // lane's first column that is exactly its right neighbour (column M)
             const float mE = act ? e : 0.0f;
@@ -782,6 +815,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         }
         cost.end(cring, tile_col(q0 + 2 * TC), tile_col(q0 + 3 * TC));
         if (out_lds || out_glb) handover(q0);
+        flush(q0);
     }
 }
 
