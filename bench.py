@@ -194,9 +194,10 @@ def main(argv=None):
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--shape", default=None,
                     help="B,N,M,D for --kernel runs (default: the headline 32,512,512,64)")
-    ap.add_argument("--numerics", choices=["fast", "exact"], default="exact",
-                    help="cell arithmetic of the recursions (exact = bit-identical to the "
-                         "reference CPU path)")
+    ap.add_argument("--numerics", choices=["mixed", "exact", "fast"], default="mixed",
+                    help="cell arithmetic of the recursions (mixed, the default: forward "
+                         "bit-identical to the reference CPU path, backward weights in fp32; "
+                         "exact: both recursions fp64-accurate)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -231,9 +232,8 @@ def main(argv=None):
 
     modes = ["unfused", "fused"] if args.mode == "both" else [args.mode]
     res = {}
-    other = {}  # the other cell arithmetic, reported beside the headline
-    alt = "fast" if args.numerics == "exact" else "exact"
-    for arith, table in ((args.numerics, res), (alt, other)):
+    others = {a: {} for a in ("mixed", "exact", "fast") if a != args.numerics}  # reported beside
+    for arith, table in [(args.numerics, res)] + list(others.items()):
         set_numerics(arith)
         for mode in modes:
             sdtw = SoftDTW(gamma=gamma, fused=(mode == "fused"))
@@ -306,8 +306,9 @@ def main(argv=None):
         "numerics": args.numerics,
         "modes": {k: {kk: (round(vv, 4) if kk != "cells_per_s" else vv) for kk, vv in v.items()}
                   for k, v in res.items()},
-        f"modes_{alt}_numerics": {k: {kk: (round(vv, 4) if kk != "cells_per_s" else vv)
-                                      for kk, vv in v.items()} for k, v in other.items()},
+        **{f"modes_{alt}_numerics": {k: {kk: (round(vv, 4) if kk != "cells_per_s" else vv)
+                                         for kk, vv in v.items()} for k, v in other.items()}
+           for alt, other in others.items()},
         "reference_ms": {"unfused": REF_UNFUSED_MS, "fused": REF_FUSED_MS,
                          "source": "bench/softdtw_memory_benchmark.csv:13 (unstated NVIDIA GPU)"},
         "roofline": roofline,

@@ -115,8 +115,10 @@ void fill_dp(DPParams& p, const DPScratch& d, int64_t B, int64_t N, int64_t M, i
 int status_of(hipError_t e) { return e == hipSuccess ? SDTW_OK : SDTW_ERR_LAUNCH; }
 
 // Process-wide cell arithmetic of the wavefront kernels (sdtw_set_numerics).
-std::atomic<int> g_numerics{SDTW_NUMERICS_EXACT};
-bool exact_numerics() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_EXACT; }
+std::atomic<int> g_numerics{SDTW_NUMERICS_MIXED};
+// forward: fp64-accurate exp / log unless FAST; backward: only in EXACT
+bool exact_forward() { return g_numerics.load(std::memory_order_relaxed) != SDTW_NUMERICS_FAST; }
+bool exact_backward() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_EXACT; }
 
 }  // namespace
 
@@ -134,10 +136,11 @@ const char* sdtw_strerror(int status) {
     }
 }
 
-int sdtw_version(void) { return 3; }
+int sdtw_version(void) { return 4; }
 
 int sdtw_set_numerics(int mode) {
-    if (mode != SDTW_NUMERICS_FAST && mode != SDTW_NUMERICS_EXACT) return -1;
+    if (mode != SDTW_NUMERICS_FAST && mode != SDTW_NUMERICS_EXACT && mode != SDTW_NUMERICS_MIXED)
+        return -1;
     return g_numerics.exchange(mode);
 }
 
@@ -277,7 +280,7 @@ int sdtw_fwd_f32(const float* D, float* R, float* out, int64_t B, int64_t N, int
     p.D = D;
     p.R = R;
     p.out = out;
-    return status_of(launch_fwd(p, false, false, exact_numerics(), (hipStream_t)stream));
+    return status_of(launch_fwd(p, false, false, exact_forward(), (hipStream_t)stream));
 }
 
 int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, int64_t B,
@@ -295,7 +298,7 @@ int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, in
     p.R = const_cast<float*>(R);
     p.gout = gout;
     p.G_out = G;
-    return status_of(launch_bwd(p, false, false, exact_numerics(), (hipStream_t)stream));
+    return status_of(launch_bwd(p, false, false, exact_backward(), (hipStream_t)stream));
 }
 
 int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int64_t B,
@@ -321,7 +324,7 @@ int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int
     p.y2 = y2;
     p.R = R;
     p.out = out;
-    return status_of(launch_fwd(p, true, small_bmm(N, M, K), exact_numerics(), st));
+    return status_of(launch_fwd(p, true, small_bmm(N, M, K), exact_forward(), st));
 }
 
 // Fused backward core: norms, then the reverse wavefront writing gout * E into `E`.
@@ -341,7 +344,7 @@ static int fused_bwd_common(const float* x, const float* y, const float* R, cons
     p.R = const_cast<float*>(R);
     p.gout = gout;
     p.G_out = E;
-    return status_of(launch_bwd(p, true, small_bmm(N, M, K), exact_numerics(), st));
+    return status_of(launch_bwd(p, true, small_bmm(N, M, K), exact_backward(), st));
 }
 
 int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const float* gout,

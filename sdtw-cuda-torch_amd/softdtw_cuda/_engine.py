@@ -23,7 +23,7 @@ _lock = threading.Lock()
 # include/sdtw.h enums
 OP_SQEUCLID_FWD, OP_SQEUCLID_BWD, OP_FWD, OP_BWD, OP_FUSED_FWD, OP_FUSED_BWD = range(6)
 DIST_EXACT, DIST_MFMA = 0, 1
-NUMERICS = {"fast": 0, "exact": 1}
+NUMERICS = {"fast": 0, "exact": 1, "mixed": 2}
 
 _SIGS = {
     "sdtw_strerror": ([ctypes.c_int], ctypes.c_char_p),
@@ -90,11 +90,15 @@ def exported_symbols():
 def set_numerics(mode: str) -> str:
     """Select the recursions' cell arithmetic for this process; returns the previous mode.
 
-    "exact" (default): the reference CPU arithmetic with fp64-accurate exp/log; R matches
-    the CPU path bit for bit and gradients meet rtol 1e-4 / atol 1e-5 against it.
-    "fast": same fp64 state, hardware fp32 exp2/log2 for the soft-min terms and backward
-    weights; forward within ~1 fp32 ulp, gradients as accurate (against an fp64
-    evaluation) as the reference's own fp32 path, faster recursions."""
+    "mixed" (default): the forward is the reference CPU arithmetic with fp64-accurate
+    exp/log, so R matches the CPU path bit for bit; the backward takes the CPU path's own
+    fp32 differences of R and D and evaluates their transition weights with the hardware
+    fp32 exp2: E within ~1e-6 relative, gradients within rtol 1e-4 / atol 1e-5.
+    "exact": fp64-accurate exp/log in both recursions; E to the last bit but for rare
+    differences.
+    "fast": hardware fp32 exp2/log2 in both recursions (fp64 state); forward within ~1 fp32
+    ulp, gradients as accurate (against an fp64 evaluation) as the reference's own fp32
+    path, but not within rtol 1e-4 of it where differences of R cancel."""
     if mode not in NUMERICS:
         raise ValueError(f"softdtw_cuda: numerics must be one of {sorted(NUMERICS)}, got {mode!r}")
     prev = load().sdtw_set_numerics(NUMERICS[mode])

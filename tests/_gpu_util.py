@@ -78,7 +78,7 @@ def engine_R_from_oracle(R_pad):
 
 @contextlib.contextmanager
 def numerics(mode):
-    """Run the block with the engine's cell arithmetic set to `mode` ("fast" / "exact")."""
+    """Run the block with the engine's cell arithmetic set to `mode` ("mixed" / "exact" / "fast")."""
     from softdtw_cuda import _engine
 
     prev = _engine.set_numerics(mode)

@@ -22,7 +22,7 @@ def _objective(bary, X, gamma=1.0):
     return float(d.mean())
 
 
-@pytest.mark.parametrize("mode", ["exact", "fast"])
+@pytest.mark.parametrize("mode", ["mixed", "exact", "fast"])
 def test_first_iteration_loss_and_gradient(mode):
     X = random_walks(KSEQ, N, D, seed=0)
     init = X.mean(dim=0)
@@ -42,9 +42,9 @@ def test_first_iteration_loss_and_gradient(mode):
             lg = (w.cuda() * SoftDTW(gamma=1.0, fused=fused)(bg.unsqueeze(0).expand(KSEQ, -1, -1), X.cuda())).sum()
             lg.backward()
         torch.testing.assert_close(lg.detach().cpu(), lo, rtol=FWD_RTOL, atol=0)
-        if mode == "exact":
+        if mode != "fast":
             v = grad_violation(bg.grad, go)
-            say(f"[bary iter0] exact fused={fused} loss {lg.item():.6f} vs {lo.item():.6f} grad violation {v:.4f}")
+            say(f"[bary iter0] {mode} fused={fused} loss {lg.item():.6f} vs {lo.item():.6f} grad violation {v:.4f}")
             assert v <= 1.0
         else:
             _, g64 = oracle_iter0(torch.float64)

@@ -1,9 +1,10 @@
 """GPU Soft-DTW recursion kernels vs the CPU oracle, given identical costs.
 
-Both cell arithmetics are checked.  exact: R bit-identical to the oracle's.  fast: R within
-1e-6 relative (the north-star forward tolerance is 1e-5) with the same infinite cells.
-Both: out within rtol 1e-5, E (= G with g = 1) within rtol 1e-4 / atol 1e-5 given the same
-D and R, and the brute-force golden vectors.
+Every cell arithmetic is checked.  exact and mixed (exact forward): R bit-identical to the
+oracle's.  fast: R within 1e-6 relative (the north-star forward tolerance is 1e-5) with the
+same infinite cells.  All: out within rtol 1e-5, E (= G with g = 1) within rtol 1e-4 /
+atol 1e-5 given the same D and R (exact: to the last bit but for rare cells; mixed: within
+rtol 1e-5 / atol 1e-7), and the brute-force golden vectors.
 """
 import json
 import os
@@ -26,7 +27,7 @@ def _golden():
         return json.load(f)["cases"]
 
 
-MODES = ["exact", "fast"]
+MODES = ["exact", "mixed", "fast"]
 
 
 @pytest.mark.parametrize("mode", MODES)
@@ -72,7 +73,7 @@ def test_dp_forward_backward_vs_oracle_same_D(B, N, M, K, gamma, bw, mode):
         E = _engine.dtw_bwd(Dg, _engine.table_pack(Rref.cuda()), gamma, bwv).cpu()
         E2 = _engine.dtw_bwd(Dg, R, gamma, bwv).cpu()
     Rc = _engine.table_unpack(R, B, N, M).cpu()
-    if mode == "exact":
+    if mode in ("exact", "mixed"):
         same = (Rc == Rref) | (torch.isinf(Rc) & torch.isinf(Rref))
         rate = same.double().mean().item()
         say(f"    R bit-equal rate {rate:.6f}")
@@ -91,6 +92,11 @@ def test_dp_forward_backward_vs_oracle_same_D(B, N, M, K, gamma, bw, mode):
         erate = (E == E_o).double().mean().item()
         say(f"    E bit-equal rate {erate:.6f}")
         assert erate >= 0.999
+    if mode == "mixed":
+        # fp32 hardware exp2 of the CPU path's own fp32 differences: ~1e-6 relative
+        vt = grad_violation(E, E_o, rtol=1e-5, atol=1e-7)
+        say(f"    mixed E violation at rtol 1e-5 / atol 1e-7: {vt:.4f}")
+        assert vt <= 1.0
     # and from the engine's own R
     v2 = grad_violation(E2, E_o)
     say(f"    E (own R) violation {v2:.4f}")
@@ -119,6 +125,9 @@ def test_numerics_switch():
         assert _engine.get_numerics() == "exact"
         assert _engine.set_numerics("fast") == "exact"
         assert _engine.get_numerics() == "fast"
+        assert _engine.set_numerics("mixed") == "fast"
+        assert _engine.load().sdtw_get_numerics() == 2
+        assert _engine.set_numerics("fast") == "mixed"
         with pytest.raises(ValueError):
             _engine.set_numerics("bf16")
         assert _engine.load().sdtw_set_numerics(7) == -1
