@@ -109,11 +109,12 @@ SDTW_DEV bool entry_empty(double v) { return row_empty(v); }
 SDTW_DEV bool entry_empty(float4 v) { return row_empty4(v); }
 
 // Spin until the LDS counter *flag >= need.  Returns false (and raises the error flag) on
-// timeout.
+// timeout.  `known` caches the last value read; every lane reads the same counter, so it is
+// kept wave-uniform (a scalar register) and the loop branches on scalar compares.
 SDTW_DEV bool wait_at_least(const int* flag, int need, int& known, int* err) {
     unsigned spins = 0;
     while (known < need) {
-        known = lds_load(flag);
+        known = __builtin_amdgcn_readfirstlane(lds_load(flag));
         if (known >= need) break;
         __builtin_amdgcn_s_sleep(1);
         if (++spins > kSpinLimit) {
@@ -121,6 +122,9 @@ SDTW_DEV bool wait_at_least(const int* flag, int need, int& known, int* err) {
             return false;
         }
     }
+    // the ring accesses the wait guards must not be moved above the counter read; the
+    // hardware performs a wave's LDS operations in order, so a compiler fence suffices
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     return true;
 }
 
@@ -256,7 +260,12 @@ struct CostD {
     // the tile is loaded at the first step and lands in the ring after the last one
     SDTW_DEV void begin(float*, int) {}
     SDTW_DEV void step(int u, int c, int) {
-        if (u == 0) issue(c);
+        if (u == 0) {
+            issue(c);
+            // keep the loads here: under register pressure the scheduler would otherwise
+            // sink them next to their stores at the group end, exposing their latency
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     SDTW_DEV void end(float* ring, int c, int) { store(ring, c); }
 };
@@ -465,14 +474,13 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     double up_cur[U], hold[U];
     float d_cur[U], d_nxt[U];
 
-    // Band above: columns [c0, c0 + U) of its last row from the LDS ring, for lane 0
-    // (+inf past M or for band 0).
+    // Band above: columns [c0, c0 + U) of its last row from the LDS ring, for lane 0.  The
+    // ring is read whether or not it waits: band 0's ring holds +inf throughout (set at
+    // kernel start, never written), and past column M - 1 lane 0 is inactive.
     auto fetch_lds = [&](int c0, double* dst) -> bool {
-#pragma unroll
-        for (int u = 0; u < U; ++u) dst[u] = INF;
-        if (b == 0 || c0 >= M) return true;
+        const bool live = b > 0 && c0 < M;
         const int need = min(c0 + U, M);
-        if (!wait_at_least(lin_flag, need, known_in, P.err)) return false;
+        if (live && !wait_at_least(lin_flag, need, known_in, P.err)) return false;
         const double2* src = reinterpret_cast<const double2*>(lin + (c0 & (RS - 1)));
 #pragma unroll
         for (int u = 0; u < U / 2; ++u) {
@@ -480,7 +488,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             dst[2 * u] = v.x;
             dst[2 * u + 1] = v.y;
         }
-        if (l == 0) lds_publish(sm.cons() + w, need);
+        if (live && l == 0) lds_publish(sm.cons() + w, need);
         return true;
     };
     // Hand the last row's columns computed by the group at s0 (lane 63 computed column
@@ -605,12 +613,17 @@ template <class Cost, bool BAND, bool EXACT>
 __global__ void __launch_bounds__(320) fwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W)};
-    const int w = threadIdx.x / WAVE;
+    // wave-uniform values are moved to scalar registers so that the branches on band,
+    // group and pair compile to scalar branches, not exec-masked regions
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;  // prod and cons are contiguous
     sm.load_tables();
+    // ring 0 starts at +inf: the padding row above band 0 (the helper wave overwrites it
+    // in workgroups that have a band above them)
+    for (int e = threadIdx.x; e < RS; e += blockDim.x) reinterpret_cast<double*>(sm.ring())[e] = dinf();
     __syncthreads();
-    const int t = *sm.ticket();
+    const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G, g = t - p * P.G;
     if (w == P.W) {  // helper wave: the previous workgroup's last row into ring 0
         if (g > 0) helper_wave(P, sm, P.gring + ((int64_t)p * P.G + (g - 1)) * P.RW + RPAD, 0);
@@ -679,14 +692,14 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 
     float4 dn_cur[U], hold[U];
     float r_cur[U], r_nxt[U], d_cur[U], d_nxt[U];
-    // padding of the reference below the table and right of it (E 0, R -inf, D 0); the
-    // fourth component is the row-entry tag (non-zero = written)
-    const float4 pad4 = make_float4(0.0f, NINF, 0.0f, 1.0f);
     // Band below: sequence numbers [q0, q0 + U) of its first row from the LDS ring, for
-    // lane 63.
+    // lane 63.  Where no band lies below, or past sequence number M - 1, the values are
+    // unused (lane 63 then holds row N - 1, which takes the padding below directly, or is
+    // beyond the table or inactive); they are set to the padding (E 0, R -inf, D 0), which
+    // compiles to fewer live registers than leaving them stale.
     auto fetch_lds = [&](int q0, float4* dst) -> bool {
 #pragma unroll
-        for (int u = 0; u < U; ++u) dst[u] = pad4;
+        for (int u = 0; u < U; ++u) dst[u] = make_float4(0.0f, NINF, 0.0f, 1.0f);
         if (b + 1 >= nb || q0 >= M) return true;
         const int need = min(q0 + U, M);
         if (!wait_at_least(lin_flag, need, known_in, P.err)) return false;
@@ -823,12 +836,14 @@ template <class Cost, bool BAND, bool EXACT>
 __global__ void __launch_bounds__(320) bwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W)};
-    const int w = threadIdx.x / WAVE;
+    // wave-uniform values are moved to scalar registers so that the branches on band,
+    // group and pair compile to scalar branches, not exec-masked regions
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;
     sm.load_tables();
     __syncthreads();
-    const int t = *sm.ticket();
+    const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G;
     const int g = (P.G - 1) - (t - p * P.G);  // lowest ticket of a pair takes the bottom group
     if (w == P.W) {  // helper wave: the next workgroup's first row into ring W
