@@ -130,6 +130,13 @@ SDTW_DEV bool wait_at_least(const int* flag, int need, int& known, int* err) {
 
 SDTW_DEV void raise_timeout(int* err) { __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
+// Slot of entry c (a column, or a backward sequence number) in an LDS handoff ring.  The
+// rotation by 63 puts the U entries a band hands over per group (c = s0 - 63 .. s0 - 48, for
+// a group starting at step s0, a multiple of U) in one aligned block of slots, so they are
+// written with immediate offsets; a consumer's group (c = c0 .. c0 + U - 1, c0 a multiple
+// of U) then reads one entry and a block of U - 1.
+SDTW_DEV int hslot(int c) { return (c + WAVE - 1) & (RS - 1); }
+
 // Soft-min of the three predecessors (diag R0, up R1, left R2) in fp64: the reference CPU
 // formula (launcher.py:317-322) restated around the minimum m as
 //   m - gamma * log(sum_k exp(-(R_k - m) / gamma)),
@@ -481,13 +488,16 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         const bool live = b > 0 && c0 < M;
         const int need = min(c0 + U, M);
         if (live && !wait_at_least(lin_flag, need, known_in, P.err)) return false;
-        const double2* src = reinterpret_cast<const double2*>(lin + (c0 & (RS - 1)));
+        const double* blk = lin + hslot(c0 + 1);  // entries c0 + 1 .. c0 + U - 1
+        dst[0] = lin[hslot(c0)];
+        const double2* src = reinterpret_cast<const double2*>(blk);
 #pragma unroll
-        for (int u = 0; u < U / 2; ++u) {
-            const double2 v = src[u];
-            dst[2 * u] = v.x;
-            dst[2 * u + 1] = v.y;
+        for (int k = 0; k < U / 2 - 1; ++k) {
+            const double2 v = src[k];
+            dst[1 + 2 * k] = v.x;
+            dst[2 + 2 * k] = v.y;
         }
+        dst[U - 1] = blk[U - 2];
         if (live && l == 0) lds_publish(sm.cons() + w, need);
         return true;
     };
@@ -499,7 +509,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         const int c0 = s0 - (WAVE - 1);
         if (out_lds) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) lout[(c0 + u) & (RS - 1)] = hold[u];
+            for (int u = 0; u < U; ++u) lout[hslot(c0) + u] = hold[u];
             lds_publish(sm.prod() + (w + 1), min(max(s0 + U - (WAVE - 1), 0), M));
         } else {
             // columns in [-63, M + 15]: inside the row's padding, no test needed
@@ -594,7 +604,7 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
         }
         const unsigned long long miss = __ballot(empty);
         const int n = miss ? (int)__builtin_ctzll(miss) : WAVE;  // leading written entries
-        if (l < n && e < M) ring[e & (RS - 1)] = v;
+        if (l < n && e < M) ring[hslot(e)] = v;
         if (n > 0) {
             c = min(c + n, M);
             if (l == 0) lds_publish(sm.prod() + k, c);
@@ -704,7 +714,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         const int need = min(q0 + U, M);
         if (!wait_at_least(lin_flag, need, known_in, P.err)) return false;
 #pragma unroll
-        for (int u = 0; u < U; ++u) dst[u] = lin[(q0 + u) & (RS - 1)];
+        for (int u = 0; u < U; ++u) dst[u] = u == 0 ? lin[hslot(q0)] : lin[hslot(q0 + 1) + u - 1];
         if (l == 0) lds_publish(sm.cons() + (w + 1), need);
         return true;
     };
@@ -716,7 +726,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         const int c0 = q0 - (WAVE - 1);
         if (out_lds) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) lout[(c0 + u) & (RS - 1)] = hold[u];
+            for (int u = 0; u < U; ++u) lout[hslot(c0) + u] = hold[u];
             lds_publish(sm.prod() + w, min(max(q0 + U - (WAVE - 1), 0), M));
         } else {
 #pragma unroll
