@@ -142,26 +142,25 @@ hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t 
 // G'(r,t) = G[t,r]).  G' is G with the clamp_min mask of the forward applied (cells whose
 // pre-clamp value was negative get 0).
 // ---------------------------------------------------------------------------------------
-template <bool MULADD>
-SDTW_DEV bool pass_mask(const DistBwdParams& p, int b, int i, int j, float d) {
-    if (d > 0.0f) return true;
-    if (!(d == 0.0f)) return false;  // NaN: clamp_min backward gives 0
-    // clamped (or exactly zero) cell: recompute the pre-clamp value
-    const float* xi = p.x + ((int64_t)b * p.N + i) * p.K;
-    const float* yj = p.y + ((int64_t)b * p.M + j) * p.K;
-    const float dot = exact_dot<MULADD>(xi, yj, p.K);
-    return exact_cost_pre(p.x2[(int64_t)b * p.N + i], p.y2[(int64_t)b * p.M + j], dot) >= 0.0f;
-}
-
-// Matrix-core version of the same product.  A workgroup owns 64 output rows x KT features
-// (KT = 16, 32 or 64); wave w computes rows 16w..16w+15 with v_mfma_f32_16x16x4_f32, the
-// reduction index t in chunks of BT staged through double-buffered LDS by coalesced loads:
-//   gs[t][r] = G'(r0 + r, t0 + t)   (A operand: 16 rows x 4 t per instruction)
-//   zs[t][k] = Z[t0 + t][k0 + k]    (B operand: 4 t x 16 features per instruction)
-// Row sums rs[r] are accumulated from the staged G' slice.  The reduction order differs
-// from the reference's matmul; gradients are compared within rtol 1e-4 / atol 1e-5.
-constexpr int BT = 32;   // reduction chunk
-constexpr int GSS = 65;  // LDS row stride of the G' slice (floats)
+// Matrix-core version of the same product.  A workgroup (4 waves) owns 64 output rows x KT
+// features (KT = 16, 32 or 64); wave w computes rows 16w..16w+15 with
+// v_mfma_f32_16x16x4_f32.  The reduction index t advances in chunks of BT = 64.  A chunk
+// is a 64 x 64 block of the (N, M) matrices G (and D, for the clamp mask) plus 64 rows of Z;
+// each thread loads its part with 16-byte loads into registers, two chunks ahead of the one
+// being multiplied, then stores it (masked) into one of two LDS buffers:
+//   gx: G'(r, t) = G[r0 + r][t0 + t] stored gT[r][t], row stride 68 floats
+//   gy: G'(r, t) = G[t0 + t][r0 + r] stored g[t][r],  row stride 80 floats
+//   Z:  zs[t][k] = Z[t0 + t][k0 + k],                 row stride 80 floats
+// With these strides the operand reads of a k-step (A: row 16w + (l & 15), t = 4kk +
+// (l >> 4); B: t = 4kk + (l >> 4), feature 16kb + (l & 15)) touch 64 distinct banks.
+// Row sums rs[r] are accumulated from the A operands.  The reduction order differs from the
+// reference's matmul; gradients are compared within rtol 1e-4 / atol 1e-5.
+constexpr int BT = 64;      // reduction chunk
+constexpr int GS_X = 68;    // gx: LDS row stride of gT (floats)
+constexpr int GS_Y = 80;    // gy: LDS row stride of g
+constexpr int ZS = 80;      // LDS row stride of zs
+constexpr int GBUF = 64 * 80;  // floats per G' buffer (the larger layout)
+constexpr int ZBUF = 64 * ZS;  // floats per Z buffer
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
@@ -172,17 +171,17 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 // gradient and resets the counter to zero for the next launch.
 template <bool TRANS, int KT, bool MULADD>
 __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int ST) {
-    constexpr int KB = KT / 16;             // 16-wide feature blocks per wave
-    constexpr int GPT = 64 * BT / 256;      // G' elements loaded per thread per chunk
-    constexpr int ZPT = BT * KT / 256;      // Z elements loaded per thread per chunk
-    static_assert(ZPT >= 1 && (BT * KT) % 256 == 0, "feature tile must feed 256 threads");
-    __shared__ float gs[2][BT][GSS];
-    __shared__ float zs[2][BT][KT + 1];
+    constexpr int KB = KT / 16;          // 16-wide feature blocks per wave
+    constexpr int ZQ = BT * KT / 1024;   // 16-byte Z loads per thread per chunk
+    static_assert(ZQ >= 1, "feature tile must feed 256 threads");
+    __shared__ __align__(16) float gbuf[2][GBUF];
+    __shared__ __align__(16) float zbuf[2][ZBUF];
     __shared__ int last_piece;
     const int b = blockIdx.z / ST, st = blockIdx.z - b * ST;
     const int r0 = blockIdx.y * 64;
     const int k0 = blockIdx.x * KT;
-    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, l = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int N = p.N, M = p.M, K = p.K;
     const int R_ = TRANS ? M : N;  // output rows
     const int T_ = TRANS ? N : M;  // reduction length
@@ -191,85 +190,142 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
     const float* Z = TRANS ? p.x + (int64_t)b * N * K : p.y + (int64_t)b * M * K;
     const float* W = TRANS ? p.y + (int64_t)b * M * K : p.x + (int64_t)b * N * K;
     float* out = TRANS ? p.gy + (int64_t)b * M * K : p.gx + (int64_t)b * N * K;
+    const bool vec_g = (M & 3) == 0;  // 16-byte loads of G / D rows are aligned
+    const bool vec_z = (K & 3) == 0;
 
-    // coalesced load of chunk t0 into registers (G' with the clamp mask applied)
-    float gv[GPT], zv[ZPT];
-    auto load_chunk = [&](int t0) {
+    // this thread's elements of a chunk: block row e4 >> 4 (of 64), columns 4 (e4 & 15) ..+3,
+    // e4 = tid + 256 q; Z: row e4 / (KT/4), features 4 (e4 % (KT/4)) ..+3
+    struct Regs {
+        float4 g[4], d[4], z[ZQ];
+    };
+    auto load_chunk = [&](int t0, Regs& R) {
+        const int a0 = TRANS ? t0 : r0, b0 = TRANS ? r0 : t0;  // block origin in (N, M)
+        const bool full = vec_g && a0 + 64 <= N && b0 + 64 <= M;
+        // uniform branches around straight-line loads: every load gets its own registers
+        if (full) {
+            const int64_t base = (int64_t)(a0 + (tid >> 4)) * M + b0 + 4 * (tid & 15);
 #pragma unroll
-        for (int q = 0; q < GPT; ++q) {
-            const int e = tid + 256 * q;
-            int r, t;
-            if (TRANS) {  // G'(r, t) = G[t][r]: contiguous along r
-                r = e & 63;
-                t = e >> 6;
-            } else {      // G'(r, t) = G[r][t]: contiguous along t
-                r = e / BT;
-                t = e % BT;
+            for (int q = 0; q < 4; ++q)
+                R.g[q] = *reinterpret_cast<const float4*>(Gb + base + (int64_t)16 * q * M);
+            if (p.mask) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    R.d[q] = *reinterpret_cast<const float4*>(Db + base + (int64_t)16 * q * M);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) R.d[q] = make_float4(1.f, 1.f, 1.f, 1.f);
             }
-            const int rr = r0 + r, tt = t0 + t;
-            float v = 0.0f;
-            if (rr < R_ && tt < T_) {
-                const int i = TRANS ? tt : rr;
-                const int j = TRANS ? rr : tt;
-                const int64_t idx = (int64_t)i * M + j;
-                v = Gb[idx];
-                if (p.mask && !pass_mask<MULADD>(p, b, i, j, Db[idx])) v = 0.0f;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int e4 = tid + 256 * q;
+                const int ia = a0 + (e4 >> 4), jb = b0 + 4 * (e4 & 15);
+                const int64_t idx = (int64_t)ia * M + jb;
+                float gv[4], dv[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const bool ok = ia < N && jb + v < M;
+                    gv[v] = ok ? Gb[idx + v] : 0.0f;
+                    dv[v] = (ok && p.mask) ? Db[idx + v] : 1.0f;
+                }
+                R.g[q] = make_float4(gv[0], gv[1], gv[2], gv[3]);
+                R.d[q] = make_float4(dv[0], dv[1], dv[2], dv[3]);
             }
-            gv[q] = v;
         }
+        const bool zfull = vec_z && t0 + BT <= T_ && k0 + KT <= K;
+        if (zfull) {
 #pragma unroll
-        for (int q = 0; q < ZPT; ++q) {
-            const int e = tid + 256 * q;
-            const int t = e / KT, k = e % KT;
-            const int tt = t0 + t, kk = k0 + k;
-            zv[q] = (tt < T_ && kk < K) ? Z[(int64_t)tt * K + kk] : 0.0f;
+            for (int q = 0; q < ZQ; ++q) {
+                const int e4 = tid + 256 * q;
+                R.z[q] = *reinterpret_cast<const float4*>(Z + (int64_t)(t0 + e4 / (KT / 4)) * K + k0 + 4 * (e4 % (KT / 4)));
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < ZQ; ++q) {
+                const int e4 = tid + 256 * q;
+                const int zt = t0 + e4 / (KT / 4), zk = k0 + 4 * (e4 % (KT / 4));
+                const int64_t idx = (int64_t)zt * K + zk;
+                float zv[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) zv[v] = (zt < T_ && zk + v < K) ? Z[idx + v] : 0.0f;
+                R.z[q] = make_float4(zv[0], zv[1], zv[2], zv[3]);
+            }
         }
     };
-    auto store_chunk = [&](int buf) {
+    // masked G' and Z into LDS buffer `buf`
+    auto store_chunk = [&](int t0, const Regs& R, int buf) {
+        const int a0 = TRANS ? t0 : r0, b0 = TRANS ? r0 : t0;
 #pragma unroll
-        for (int q = 0; q < GPT; ++q) {
-            const int e = tid + 256 * q;
-            const int r = TRANS ? (e & 63) : (e / BT);
-            const int t = TRANS ? (e >> 6) : (e % BT);
-            gs[buf][t][r] = gv[q];
+        for (int q = 0; q < 4; ++q) {
+            const int e4 = tid + 256 * q;
+            const int br = e4 >> 4, bc = 4 * (e4 & 15);
+            float g4[4] = {R.g[q].x, R.g[q].y, R.g[q].z, R.g[q].w};
+            const float d4[4] = {R.d[q].x, R.d[q].y, R.d[q].z, R.d[q].w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (d4[v] > 0.0f) continue;  // passes (also the padding, d = 1)
+                // d = 0 or NaN: clamp_min passes where the pre-clamp value is >= 0
+                const int i = a0 + br, j = b0 + bc + v;
+                bool pass = false;
+                if (d4[v] == 0.0f && i < N && j < M) {
+                    const float dot = exact_dot<MULADD>(p.x + ((int64_t)b * N + i) * K, p.y + ((int64_t)b * M + j) * K, K);
+                    pass = exact_cost_pre(p.x2[(int64_t)b * N + i], p.y2[(int64_t)b * M + j], dot) >= 0.0f;
+                }
+                if (!pass) g4[v] = 0.0f;
+            }
+            if (TRANS) {  // block row = t, columns = r: g[t][r..r+3]
+                *reinterpret_cast<float4*>(&gbuf[buf][br * GS_Y + bc]) = make_float4(g4[0], g4[1], g4[2], g4[3]);
+            } else {      // block row = r, columns = t: gT[r][t..t+3]
+                *reinterpret_cast<float4*>(&gbuf[buf][br * GS_X + bc]) = make_float4(g4[0], g4[1], g4[2], g4[3]);
+            }
         }
 #pragma unroll
-        for (int q = 0; q < ZPT; ++q) {
-            const int e = tid + 256 * q;
-            zs[buf][e / KT][e % KT] = zv[q];
+        for (int q = 0; q < ZQ; ++q) {
+            const int e4 = tid + 256 * q;
+            *reinterpret_cast<float4*>(&zbuf[buf][(e4 / (KT / 4)) * ZS + 4 * (e4 % (KT / 4))]) = R.z[q];
         }
     };
 
     floatx4_t acc[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) acc[kb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float rs_part = 0.0f;  // row 16w + (l & 15), t = (l >> 4) * BT/4 .. of each chunk
+    float rs_part = 0.0f;  // row 16w + (l & 15), t = 4kk + (l >> 4) of every k-step
+    auto multiply = [&](int buf) {
+        const float* gb = gbuf[buf];
+        const float* zb = zbuf[buf];
+#pragma unroll
+        for (int kk = 0; kk < BT / 4; ++kk) {
+            const int t = 4 * kk + (l >> 4), r = 16 * w + (l & 15);
+            const float a = TRANS ? gb[t * GS_Y + r] : gb[r * GS_X + t];
+            rs_part += a;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const float bv = zb[t * ZS + 16 * kb + (l & 15)];
+                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[kb], 0, 0, 0);
+            }
+        }
+    };
 
     const int total = (T_ + BT - 1) / BT;
     const int cps = (total + ST - 1) / ST;
     const int cbeg = min(st * cps, total), cend = min(cbeg + cps, total);
     const int nchunks = cend - cbeg;
-    if (nchunks > 0) {
-        load_chunk(cbeg * BT);
-        store_chunk(0);
-    }
-    __syncthreads();
-    for (int c = 0; c < nchunks; ++c) {
-        const int buf = c & 1;
-        if (c + 1 < nchunks) load_chunk((cbeg + c + 1) * BT);  // in flight during the products
-#pragma unroll
-        for (int q = 0; q < BT / 4; ++q) rs_part += gs[buf][(l >> 4) * (BT / 4) + q][16 * w + (l & 15)];
-#pragma unroll
-        for (int kk = 0; kk < BT / 4; ++kk) {
-            const float a = gs[buf][4 * kk + (l >> 4)][16 * w + (l & 15)];
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                const float bv = zs[buf][4 * kk + (l >> 4)][16 * kb + (l & 15)];
-                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[kb], 0, 0, 0);
-            }
-        }
-        if (c + 1 < nchunks) store_chunk(buf ^ 1);
+    // pipeline: chunk c is stored from registers set c & 1, whose loads for chunk c + 2 are
+    // issued right after; the products of chunk c run from LDS buffer c & 1
+    Regs ra, rb;
+    if (nchunks > 0) load_chunk(cbeg * BT, ra);
+    if (nchunks > 1) load_chunk((cbeg + 1) * BT, rb);
+    for (int c = 0; c < nchunks; c += 2) {
+        store_chunk((cbeg + c) * BT, ra, 0);
+        if (c + 2 < nchunks) load_chunk((cbeg + c + 2) * BT, ra);
         __syncthreads();
+        multiply(0);
+        if (c + 1 < nchunks) {
+            store_chunk((cbeg + c + 1) * BT, rb, 1);
+            if (c + 3 < nchunks) load_chunk((cbeg + c + 3) * BT, rb);
+            __syncthreads();
+            multiply(1);
+        }
     }
     // rs of row 16w + x: sum of the four lanes with (l & 15) == x
     float rs = rs_part + __shfl_xor(rs_part, 16);
@@ -348,7 +404,8 @@ static void launch_dist_bwd_one(const DistBwdParams& p, hipStream_t st) {
 }
 
 hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st) {
-    if (p.part) {  // counters start at zero; every pass leaves them at zero
+    const bool split = p.part && (dist_bwd_splits(p.B, p.N, p.M, p.K) > 1 || dist_bwd_splits(p.B, p.M, p.N, p.K) > 1);
+    if (split) {  // counters start at zero; every pass leaves them at zero
         const int64_t n = dist_bwd_counters(p.B, p.N, p.M, p.K);
         const int blocks = (int)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
         hipLaunchKernelGGL(zero_ints_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, st, p.cnt, n);

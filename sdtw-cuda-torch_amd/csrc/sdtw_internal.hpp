@@ -54,15 +54,16 @@ struct DistBwdParams {
 };
 
 // Split reduction of the distance backward: the reduction of a 64-row x KT-feature output
-// tile is cut into dist_bwd_splits() pieces so that about 1024 workgroups are in flight.
+// tile is cut into dist_bwd_splits() pieces (of whole 64-wide chunks) so that about 256
+// workgroups, one per CU, are in flight.
 inline int dist_bwd_kt(int64_t K) { return K <= 16 ? 16 : (K <= 32 ? 32 : 64); }
 inline int64_t dist_bwd_tiles(int64_t B, int64_t R, int64_t K) {
     return B * ((R + 63) / 64) * ((K + dist_bwd_kt(K) - 1) / dist_bwd_kt(K));
 }
 inline int dist_bwd_splits(int64_t B, int64_t R, int64_t T, int64_t K) {
     const int64_t tiles = dist_bwd_tiles(B, R, K);
-    const int64_t chunks = (T + 31) / 32;
-    int64_t st = (1024 + tiles - 1) / tiles;
+    const int64_t chunks = (T + 63) / 64;
+    int64_t st = (256 + tiles - 1) / tiles;
     st = st > 8 ? 8 : st;
     st = st > chunks ? chunks : st;
     return (int)(st < 1 ? 1 : st);
