@@ -8,6 +8,8 @@
 //                     gx = 2 (x * rowsum(G') - G' y) and gy = 2 (y * colsum(G') - G'^T x)
 //                     on the matrix cores, with G' = G masked by the clamp (clamp_min
 //                     backward passes where x2 + y2 - 2xy >= 0).
+#include <type_traits>
+
 #include "sdtw_device.hpp"
 #include "sdtw_internal.hpp"
 
@@ -63,9 +65,15 @@ template <bool MULADD>
 __global__ void __launch_bounds__(256) dist_kernel(DistParams p) {
     __shared__ float xs[KC][DT + 1];
     __shared__ float ys[KC][DT + 1];
-    const int b = blockIdx.z;
-    const int i0 = blockIdx.y * DT;
-    const int j0 = blockIdx.x * DT;
+    // XCD-aware tile order (workgroups go to the 8 XCDs round-robin by linear id): the
+    // tiles of one pair, which read the same rows of x and y, run on one XCD's L2
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int nwg = gx * gy * gridDim.z;
+    const int id = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const int v = (nwg & 7) == 0 ? (id & 7) * (nwg >> 3) + (id >> 3) : id;
+    const int b = v / (gx * gy);
+    const int i0 = ((v / gx) % gy) * DT;
+    const int j0 = (v % gx) * DT;
     const int tx = threadIdx.x & 15;
     const int ty = threadIdx.x >> 4;
     const int N = p.N, M = p.M, K = p.K;
@@ -142,6 +150,14 @@ hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t 
 // G'(r,t) = G[t,r]).  G' is G with the clamp_min mask of the forward applied (cells whose
 // pre-clamp value was negative get 0).
 // ---------------------------------------------------------------------------------------
+// Whether the clamp_min mask passes a cell whose clamped cost is 0: its pre-clamp value
+// x2 + y2 - 2 x.y (recomputed with the forward's bits) is >= 0.  Rare (x_i ~ y_j).
+template <bool MULADD>
+SDTW_DEV bool clamp_passes(const DistBwdParams& p, int b, int i, int j) {
+    const float dot = exact_dot<MULADD>(p.x + ((int64_t)b * p.N + i) * p.K, p.y + ((int64_t)b * p.M + j) * p.K, p.K);
+    return exact_cost_pre(p.x2[(int64_t)b * p.N + i], p.y2[(int64_t)b * p.M + j], dot) >= 0.0f;
+}
+
 // Matrix-core version of the same product.  A workgroup (4 waves) owns 64 output rows x KT
 // features (KT = 16, 32 or 64); wave w computes rows 16w..16w+15 with
 // v_mfma_f32_16x16x4_f32.  The reduction index t advances in chunks of BT = 64.  A chunk
@@ -164,12 +180,13 @@ constexpr int ZBUF = 64 * ZS;  // floats per Z buffer
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-// Split reduction: blockIdx.z = b * ST + st; piece st takes chunks [st*cps, (st+1)*cps).
+// Split reduction: z = b * ST + st (z after the XCD remap below); piece st takes chunks
+// [st*cps, (st+1)*cps).
 // With ST > 1 every piece stores W*rs - acc of its chunks as a partial (device-coherent
 // stores), waits for them to complete and counts itself in the tile's counter; the last
 // piece to arrive adds the ST partials in order 0..ST-1 (deterministic), writes the
 // gradient and resets the counter to zero for the next launch.
-template <bool TRANS, int KT, bool MULADD>
+template <bool TRANS, int KT, bool MULADD, bool MASK>
 __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int ST) {
     constexpr int KB = KT / 16;          // 16-wide feature blocks per wave
     constexpr int ZQ = BT * KT / 1024;   // 16-byte Z loads per thread per chunk
@@ -177,9 +194,21 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
     __shared__ __align__(16) float gbuf[2][GBUF];
     __shared__ __align__(16) float zbuf[2][ZBUF];
     __shared__ int last_piece;
-    const int b = blockIdx.z / ST, st = blockIdx.z - b * ST;
-    const int r0 = blockIdx.y * 64;
-    const int k0 = blockIdx.x * KT;
+    // Workgroups are dispatched to the 8 XCDs round-robin by linear id; the id is remapped
+    // so that consecutive tiles (the row strips of one pair, which read the same Z) run on
+    // the same XCD and share its L2.
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int nwg = gx * gy * gridDim.z;
+    const int id = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const int v = (nwg & 7) == 0 ? (id & 7) * (nwg >> 3) + (id >> 3) : id;
+    // integer divisions expand to vector code: pin the (uniform) results to scalar registers
+    // so that the pipeline loop below is a uniform loop
+    const int bx = __builtin_amdgcn_readfirstlane(v % gx);
+    const int by = __builtin_amdgcn_readfirstlane((v / gx) % gy);
+    const int bz = __builtin_amdgcn_readfirstlane(v / (gx * gy));
+    const int b = __builtin_amdgcn_readfirstlane(bz / ST), st = bz - b * ST;
+    const int r0 = by * 64;
+    const int k0 = bx * KT;
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int N = p.N, M = p.M, K = p.K;
@@ -198,42 +227,48 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
     struct Regs {
         float4 g[4], d[4], z[ZQ];
     };
-    auto load_chunk = [&](int t0, Regs& R) {
+    // Two load paths, chosen per workgroup at compile time (a loop mixing them would make
+    // the compiler wait for every load in flight): FG, every chunk a full 64 x 64 block of
+    // rows of length M % 4 == 0, loaded as 16-byte vectors; else element by element with
+    // bounds.  ZF likewise for Z (K % 4 == 0 and K % KT == 0).  D is read only with MASK.
+    auto load_chunk = [&](int t0, Regs& R, auto fg_tag, auto zf_tag) {
+        constexpr bool FG = decltype(fg_tag)::value, ZF = decltype(zf_tag)::value;
         const int a0 = TRANS ? t0 : r0, b0 = TRANS ? r0 : t0;  // block origin in (N, M)
-        const bool full = vec_g && a0 + 64 <= N && b0 + 64 <= M;
-        // uniform branches around straight-line loads: every load gets its own registers
-        if (full) {
+        if (FG) {
             const int64_t base = (int64_t)(a0 + (tid >> 4)) * M + b0 + 4 * (tid & 15);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < 4; ++q) {
                 R.g[q] = *reinterpret_cast<const float4*>(Gb + base + (int64_t)16 * q * M);
-            if (p.mask) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    R.d[q] = *reinterpret_cast<const float4*>(Db + base + (int64_t)16 * q * M);
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) R.d[q] = make_float4(1.f, 1.f, 1.f, 1.f);
+                R.d[q] = MASK ? *reinterpret_cast<const float4*>(Db + base + (int64_t)16 * q * M)
+                              : make_float4(1.f, 1.f, 1.f, 1.f);
             }
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int e4 = tid + 256 * q;
                 const int ia = a0 + (e4 >> 4), jb = b0 + 4 * (e4 & 15);
-                const int64_t idx = (int64_t)ia * M + jb;
+                const int64_t row = (int64_t)min(ia, N - 1) * M;
                 float gv[4], dv[4];
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
+                    // unconditional load from a clamped index, then a select: a fixed number
+                    // of loads per chunk keeps the compiler's load accounting exact
                     const bool ok = ia < N && jb + v < M;
-                    gv[v] = ok ? Gb[idx + v] : 0.0f;
-                    dv[v] = (ok && p.mask) ? Db[idx + v] : 1.0f;
+                    const int64_t idx = row + min(jb + v, M - 1);
+                    const float gl = Gb[idx];
+                    gv[v] = ok ? gl : 0.0f;
+                    if (MASK) {
+                        const float dl = Db[idx];
+                        dv[v] = ok ? dl : 1.0f;
+                    } else {
+                        dv[v] = 1.0f;
+                    }
                 }
                 R.g[q] = make_float4(gv[0], gv[1], gv[2], gv[3]);
                 R.d[q] = make_float4(dv[0], dv[1], dv[2], dv[3]);
             }
         }
-        const bool zfull = vec_z && t0 + BT <= T_ && k0 + KT <= K;
-        if (zfull) {
+        if (ZF) {
 #pragma unroll
             for (int q = 0; q < ZQ; ++q) {
                 const int e4 = tid + 256 * q;
@@ -244,16 +279,26 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
             for (int q = 0; q < ZQ; ++q) {
                 const int e4 = tid + 256 * q;
                 const int zt = t0 + e4 / (KT / 4), zk = k0 + 4 * (e4 % (KT / 4));
-                const int64_t idx = (int64_t)zt * K + zk;
+                const int64_t row = (int64_t)min(zt, T_ - 1) * K;
                 float zv[4];
 #pragma unroll
-                for (int v = 0; v < 4; ++v) zv[v] = (zt < T_ && zk + v < K) ? Z[idx + v] : 0.0f;
+                for (int v = 0; v < 4; ++v) {
+                    const float z = Z[row + min(zk + v, K - 1)];
+                    zv[v] = (zt < T_ && zk + v < K) ? z : 0.0f;
+                }
                 R.z[q] = make_float4(zv[0], zv[1], zv[2], zv[3]);
             }
         }
     };
-    // masked G' and Z into LDS buffer `buf`
-    auto store_chunk = [&](int t0, const Regs& R, int buf) {
+    // Masked G' and Z into LDS buffer `buf`.  Cells whose clamped cost is positive pass the
+    // clamp_min mask, NaN ones do not.  A cost of exactly 0 passes only where the pre-clamp
+    // value was >= 0: the first pass (EXACT false) masks such cells and records that it
+    // saw one, and a workgroup that saw one reruns with the exact per-cell check (loads of
+    // x and y rows inside the pipeline, hence slower).  Keeping loads out of the first pass
+    // lets the compiler wait on each chunk's loads alone.
+    bool zero_seen = false;
+    auto store_chunk = [&](int t0, const Regs& R, int buf, auto exact_tag) {
+        constexpr bool EXACT = MASK && decltype(exact_tag)::value;
         const int a0 = TRANS ? t0 : r0, b0 = TRANS ? r0 : t0;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -263,15 +308,15 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
             const float d4[4] = {R.d[q].x, R.d[q].y, R.d[q].z, R.d[q].w};
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                if (d4[v] > 0.0f) continue;  // passes (also the padding, d = 1)
-                // d = 0 or NaN: clamp_min passes where the pre-clamp value is >= 0
                 const int i = a0 + br, j = b0 + bc + v;
-                bool pass = false;
-                if (d4[v] == 0.0f && i < N && j < M) {
-                    const float dot = exact_dot<MULADD>(p.x + ((int64_t)b * N + i) * K, p.y + ((int64_t)b * M + j) * K, K);
-                    pass = exact_cost_pre(p.x2[(int64_t)b * N + i], p.y2[(int64_t)b * M + j], dot) >= 0.0f;
+                if (EXACT) {
+                    if (!(d4[v] > 0.0f) &&  // positive passes (also the padding, d = 1)
+                        !(d4[v] == 0.0f && i < N && j < M && clamp_passes<MULADD>(p, b, i, j)))
+                        g4[v] = 0.0f;
+                } else {  // selects only: no branch, no load
+                    zero_seen |= d4[v] == 0.0f && i < N && j < M;
+                    g4[v] = d4[v] > 0.0f ? g4[v] : 0.0f;
                 }
-                if (!pass) g4[v] = 0.0f;
             }
             if (TRANS) {  // block row = t, columns = r: g[t][r..r+3]
                 *reinterpret_cast<float4*>(&gbuf[buf][br * GS_Y + bc]) = make_float4(g4[0], g4[1], g4[2], g4[3]);
@@ -290,43 +335,92 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) acc[kb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float rs_part = 0.0f;  // row 16w + (l & 15), t = 4kk + (l >> 4) of every k-step
+    // operands of k-step kk + 1 are read before the products of k-step kk are issued, so the
+    // LDS latency overlaps the matrix pipe (the scheduling barriers keep that order)
     auto multiply = [&](int buf) {
         const float* gb = gbuf[buf];
         const float* zb = zbuf[buf];
+        auto read_ops = [&](int kk, float& a, float* bv) {
+            const int t = 4 * kk + (l >> 4), r = 16 * w + (l & 15);
+            a = TRANS ? gb[t * GS_Y + r] : gb[r * GS_X + t];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) bv[kb] = zb[t * ZS + 16 * kb + (l & 15)];
+        };
+        float a_c, b_c[KB];
+        read_ops(0, a_c, b_c);
 #pragma unroll
         for (int kk = 0; kk < BT / 4; ++kk) {
-            const int t = 4 * kk + (l >> 4), r = 16 * w + (l & 15);
-            const float a = TRANS ? gb[t * GS_Y + r] : gb[r * GS_X + t];
-            rs_part += a;
+            float a_n = 0.0f, b_n[KB];
+            if (kk + 1 < BT / 4) read_ops(kk + 1, a_n, b_n);
+            __builtin_amdgcn_sched_barrier(0);
+            rs_part += a_c;
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                const float bv = zb[t * ZS + 16 * kb + (l & 15)];
-                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[kb], 0, 0, 0);
-            }
+            for (int kb = 0; kb < KB; ++kb)
+                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a_c, b_c[kb], acc[kb], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            a_c = a_n;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) b_c[kb] = b_n[kb];
         }
     };
 
     const int total = (T_ + BT - 1) / BT;
-    const int cps = (total + ST - 1) / ST;
-    const int cbeg = min(st * cps, total), cend = min(cbeg + cps, total);
-    const int nchunks = cend - cbeg;
-    // pipeline: chunk c is stored from registers set c & 1, whose loads for chunk c + 2 are
-    // issued right after; the products of chunk c run from LDS buffer c & 1
-    Regs ra, rb;
-    if (nchunks > 0) load_chunk(cbeg * BT, ra);
-    if (nchunks > 1) load_chunk((cbeg + 1) * BT, rb);
-    for (int c = 0; c < nchunks; c += 2) {
-        store_chunk((cbeg + c) * BT, ra, 0);
-        if (c + 2 < nchunks) load_chunk((cbeg + c + 2) * BT, ra);
-        __syncthreads();
-        multiply(0);
-        if (c + 1 < nchunks) {
-            store_chunk((cbeg + c + 1) * BT, rb, 1);
-            if (c + 3 < nchunks) load_chunk((cbeg + c + 3) * BT, rb);
+    const int cps = __builtin_amdgcn_readfirstlane((total + ST - 1) / ST);
+    const int cbeg = __builtin_amdgcn_readfirstlane(min(st * cps, total));
+    const int nchunks = __builtin_amdgcn_readfirstlane(min(cbeg + cps, total) - cbeg);
+    // Pipeline: chunk c is stored from register set c & 1, whose loads for chunk c + 2 are
+    // issued right after; the products of chunk c run from LDS buffer c & 1.  The steady
+    // state loads unconditionally (a register set conditionally reloaded inside the loop
+    // would be copied between iterations, and a copy waits for every load in flight); the
+    // last two to three chunks are an explicit epilogue.
+    auto run = [&](auto exact_tag, auto fg, auto zf) {
+        Regs ra, rb;
+        if (nchunks > 0) load_chunk(cbeg * BT, ra, fg, zf);
+        if (nchunks > 1) load_chunk((cbeg + 1) * BT, rb, fg, zf);
+        int c = 0;
+        for (; c + 3 < nchunks; c += 2) {
+            store_chunk((cbeg + c) * BT, ra, 0, exact_tag);
+            load_chunk((cbeg + c + 2) * BT, ra, fg, zf);
+            __syncthreads();
+            multiply(0);
+            store_chunk((cbeg + c + 1) * BT, rb, 1, exact_tag);
+            load_chunk((cbeg + c + 3) * BT, rb, fg, zf);
             __syncthreads();
             multiply(1);
         }
+        const int rem = nchunks - c;  // 0 .. 3
+        if (rem >= 1) {
+            store_chunk((cbeg + c) * BT, ra, 0, exact_tag);
+            if (rem == 3) load_chunk((cbeg + c + 2) * BT, ra, fg, zf);
+            __syncthreads();
+            multiply(0);
+        }
+        if (rem >= 2) {
+            store_chunk((cbeg + c + 1) * BT, rb, 1, exact_tag);
+            __syncthreads();
+            multiply(1);
+        }
+        if (rem == 3) {
+            store_chunk((cbeg + c + 2) * BT, ra, 0, exact_tag);
+            __syncthreads();
+            multiply(0);
+        }
+    };
+    const bool fg = vec_g && r0 + 64 <= R_ && T_ % BT == 0;
+    const bool zf = vec_z && K % KT == 0 && T_ % BT == 0;
+    auto run_any = [&](auto exact_tag) {
+        if (fg && zf) run(exact_tag, std::true_type{}, std::true_type{});
+        else if (fg) run(exact_tag, std::true_type{}, std::false_type{});
+        else run(exact_tag, std::false_type{}, std::false_type{});
+    };
+    run_any(std::false_type{});
+    if (MASK && __syncthreads_or(zero_seen)) {  // rare: rerun the tile with the exact mask
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) acc[kb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        rs_part = 0.0f;
+        run_any(std::true_type{});
     }
+
     // rs of row 16w + x: sum of the four lanes with (l & 15) == x
     float rs = rs_part + __shfl_xor(rs_part, 16);
     rs = rs + __shfl_xor(rs, 32);
@@ -344,7 +438,7 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
         }
     }
     if (ST > 1) {
-        const int64_t tile = ((int64_t)b * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        const int64_t tile = ((int64_t)b * gy + by) * gx + bx;
         float* part = p.part + tile * ST * 64 * KT;
         // partial of piece st: element (row 16w + 4(l>>4) + v, feature 16kb + (l&15))
         auto pidx = [&](int q, int v, int kb) {
@@ -395,12 +489,21 @@ static void launch_dist_bwd_one(const DistBwdParams& p, hipStream_t st) {
     const int KT = dist_bwd_kt(p.K);
     const int ST = p.part ? dist_bwd_splits(p.B, R_, T_, p.K) : 1;
     dim3 grid((p.K + KT - 1) / KT, (R_ + 63) / 64, p.B * ST);
-    if (KT == 16)
-        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 16, MULADD>), grid, dim3(256), 0, st, p, ST);
-    else if (KT == 32)
-        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 32, MULADD>), grid, dim3(256), 0, st, p, ST);
-    else
-        hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 64, MULADD>), grid, dim3(256), 0, st, p, ST);
+    if (p.mask) {
+        if (KT == 16)
+            hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 16, MULADD, true>), grid, dim3(256), 0, st, p, ST);
+        else if (KT == 32)
+            hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 32, MULADD, true>), grid, dim3(256), 0, st, p, ST);
+        else
+            hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 64, MULADD, true>), grid, dim3(256), 0, st, p, ST);
+    } else {
+        if (KT == 16)
+            hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 16, MULADD, false>), grid, dim3(256), 0, st, p, ST);
+        else if (KT == 32)
+            hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 32, MULADD, false>), grid, dim3(256), 0, st, p, ST);
+        else
+            hipLaunchKernelGGL((dist_bwd_mfma_kernel<TRANS, 64, MULADD, false>), grid, dim3(256), 0, st, p, ST);
+    }
 }
 
 hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st) {
