@@ -137,30 +137,30 @@ SDTW_DEV void raise_timeout(int* err) { __hip_atomic_store(err, 1, __ATOMIC_RELA
 // of U) then reads one entry and a block of U - 1.
 SDTW_DEV int hslot(int c) { return (c + WAVE - 1) & (RS - 1); }
 
-// Soft-min of the three predecessors (diag R0, up R1, left R2) in fp64: the reference CPU
-// formula (launcher.py:317-322) restated around the minimum m as
-//   m - gamma * log(sum_k exp(-(R_k - m) / gamma)),
-// summed in the reference's index order ((t0 + t1) + t2).  The minimum's term is exactly 1,
-// so only the other two exponentials are evaluated; with the first minimum at index a,
-//   a = 0 or 1: (1 + e_first) + e_second,   a = 2: (e_first + e_second) + 1,
-// the same sums as the reference's.  exp / log are the table-driven fp64 ones (T, L in
-// LDS).  Min and maxNum drop NaN operands, so NaN is put back explicitly: `nanfix` is NaN
-// when an input is NaN or all three are +inf (where the reference's expression evaluates
-// inf - inf), else 0.
-SDTW_DEV double softmin_exact(double R0, double R1, double R2, double gamma, double inv_gamma,
-                              double& nanfix, const double* T, const double* L) {
+// One forward cell: d + soft-min of the three predecessors (diag R0, up R1, left R2) in fp64,
+// the reference CPU formula (launcher.py:317-322) restated around the minimum m as
+//   m - gamma * log(sum_k exp(-(R_k - m) / gamma)).
+// The minimum's term is exactly 1, so only the exponentials of the other two predecessors
+// (R_a, R_b, in index order) are evaluated, and the sum is (e_a + e_b) + 1.  exp / log are
+// the table-driven fp64 ones (T, L in LDS); every intermediate is fp64-accurate and R is
+// rounded once to fp32 by the caller, which is what makes R equal the CPU path's bits.
+// Min and maxNum drop NaN operands, so NaN is put back explicitly: `nanfix` is NaN when an
+// input is NaN (R0 + R1 + R2 is then NaN: R is never -inf from a cost >= 0) or all three are
+// +inf (where the reference's expression evaluates inf - inf), else 0.  d + m + nanfix is
+// formed off the exponential chain.
+SDTW_DEV double fwd_cell_exact(double R0, double R1, double R2, float d, double gamma, double inv_gamma,
+                               const double* T, const double* L) {
     const double m = fmin(fmin(R0, R1), R2);
-    const bool nan_in = (R0 != R0) || (R1 != R1) || (R2 != R2);
-    nanfix = (m - m) + (nan_in ? __builtin_nan("") : 0.0);
+    const double sum3 = (R0 + R1) + R2;
+    const double nanfix = (m - m) + (sum3 != sum3 ? __builtin_nan("") : 0.0);
     const bool a0 = (R0 == m);
     const bool a2 = !a0 && !(R1 == m);
-    const double Ra = a0 ? R1 : R0;  // the two other predecessors, in index order
+    const double Ra = a0 ? R1 : R0;
     const double Rb = a2 ? R1 : R2;
     const double ea = fm::exp_tab((m - Ra) * inv_gamma, T);
     const double eb = fm::exp_tab((m - Rb) * inv_gamma, T);
-    const double p = a2 ? eb : 1.0, q = a2 ? 1.0 : eb;
-    const double rsum = (ea + p) + q;
-    return fma(-gamma, fm::log_tab_1to3(rsum, L), m);
+    const double rsum = (ea + eb) + 1.0;
+    return fma(-gamma, fm::log_tab_1to3(rsum, L), ((double)d + m) + nanfix);
 }
 
 // One backward cell (launcher.py:347-351): fp32 differences, fp64 exp/products/sum (in the
@@ -413,9 +413,9 @@ struct CostScalar {
 };
 
 // shared-memory layout of the DP kernels:
-//   [ticket, counters 256 B][exp / log tables 1536 B][handoff rings][cost rings]
+//   [ticket, counters 256 B][exp / log tables 2560 B][handoff rings][cost rings]
 // W + 1 produced/consumed counter pairs, one per handoff ring
-constexpr int kTabBytes = (64 + 128) * 8;
+constexpr int kTabBytes = (64 + 256) * 8;
 struct Smem {
     unsigned char* base;
     int W;
@@ -431,7 +431,7 @@ struct Smem {
     // every thread of the workgroup, before the first barrier
     SDTW_DEV void load_tables() const {
         double* t = tables();
-        for (int e = threadIdx.x; e < 64 + 128; e += blockDim.x)
+        for (int e = threadIdx.x; e < 64 + 256; e += blockDim.x)
             t[e] = e < 64 ? fm::kExp2Tab[e] : fm::kLogTab[e - 64];
     }
 };
@@ -553,9 +553,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             const double up = shr1(up_cur[u], prev);
             double cand;
             if (EXACT) {
-                double nanfix;
-                const double sm_ = softmin_exact(diag, up, left, gamma, inv_gamma, nanfix, tabE, tabL);
-                cand = ((double)d_cur[u] + sm_) + nanfix;
+                cand = fwd_cell_exact(diag, up, left, d_cur[u], gamma, inv_gamma, tabE, tabL);
             } else {
                 cand = fwd_cell_hw(diag, up, left, d_cur[u], c2, ngl);
             }
