@@ -34,6 +34,8 @@
 //         gamma*log(3) per cell, so R stays within ~1 fp32 ulp of the exact recursion.
 #pragma once
 
+#include <type_traits>
+
 #include "sdtw_device.hpp"
 #include "sdtw_internal.hpp"
 #include "sdtw_math.hpp"
@@ -778,18 +780,27 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         d_nxt[u] = crow[ring_col(u)];
     }
 
-    for (int q0 = 0; q0 < S; q0 += U) {
+    // One group: 16 reverse steps from q0.  INTERIOR: every lane is inside the table for all
+    // of them (a band with a band below it, columns M + 62 - q0 .. M - 16 - q0 within [0, M),
+    // no Sakoe-Chiba band), so no cell needs the padding row or the inactive masking.  The
+    // interior groups form one run of q0, walked by a loop of its own (three loops in
+    // sequence rather than a branch per group, which would join the loop-carried registers
+    // of two bodies).  Only with costs from the distance matrix: with a tile-computing cost
+    // provider the extra body costs more registers than it saves.
+    auto group = [&](int q0, auto interior_tag) -> bool {
+        constexpr bool INTERIOR = decltype(interior_tag)::value;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             r_cur[u] = r_nxt[u];
             d_cur[u] = d_nxt[u];
         }
         cost.begin(cring, tile_col(q0 + 2 * TC));
-        if (!fetch_lds(q0, dn_cur)) return;
+        if (!fetch_lds(q0, dn_cur)) return false;
         const int n0 = q0 + U;
         if (out_lds) {  // as in the forward: sequence numbers up to q0 + U - 64 this group
             const int need_free = q0 + U - WAVE + 1 - RS;
-            if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err)) return;
+            if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err))
+                return false;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -798,19 +809,19 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             float dE = __int_as_float(dpp_shl1(__float_as_int(dn_cur[u].x), __float_as_int(pE)));
             float dR = __int_as_float(dpp_shl1(__float_as_int(dn_cur[u].y), __float_as_int(pR)));
             float dD = __int_as_float(dpp_shl1(__float_as_int(dn_cur[u].z), __float_as_int(pD)));
-            if (last_row) {  // the padded row below the table
+            if (!INTERIOR && last_row) {  // the padded row below the table
                 const bool corner = (j == M);
                 dE = corner ? 1.0f : 0.0f;
                 dR = corner ? corner_R : NINF;
                 dD = 0.0f;
             }
-            const bool act = row_ok && (unsigned)j < (unsigned)M;
+            const bool act = INTERIOR || (row_ok && (unsigned)j < (unsigned)M);
             float rij = r_cur[u];
             rij = __builtin_isinf(rij) ? NINF : rij;
             const float cand = EXACT ? bwd_cell_exact(rij, dE, dR, dD, rE, rR, rD, gE, gR, gD, inv_gamma, tabE)
                                      : bwd_cell_hw(rij, dE, dR, dD, rE, rR, rD, gE, gR, gD, c2);
             bool keep = true;
-            if (BAND) keep = !out_of_band(bw, i, j);
+            if (BAND && !INTERIOR) keep = !out_of_band(bw, i, j);
             const float e = keep ? cand : 0.0f;
             crow[j & (CR - 1)] = __fmul_rn(gsc, e);
             // inactive steps carry the reference's padding (E 0, R -inf, D 0): before a
@@ -837,7 +848,20 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         cost.end(cring, tile_col(q0 + 2 * TC), tile_col(q0 + 3 * TC));
         if (out_lds || out_glb) handover(q0);
         flush(q0);
+        return true;
+    };
+    int q0 = 0;
+    if constexpr (!BAND && std::is_same<Cost, CostD>::value) {
+        const bool has_interior = b + 1 < nb;
+        const int q_in = has_interior ? WAVE : S;
+        const int q_out = has_interior ? max(((M - U) / U + 1) * U, WAVE) : S;
+        for (; q0 < q_in; q0 += U)
+            if (!group(q0, std::false_type{})) return;
+        for (; q0 < q_out; q0 += U)
+            if (!group(q0, std::true_type{})) return;
     }
+    for (; q0 < S; q0 += U)
+        if (!group(q0, std::false_type{})) return;
 }
 
 template <class Cost, bool BAND, bool EXACT>
