@@ -215,13 +215,11 @@ int sdtw_sqeuclid_fwd_f32(const float* x, const float* y, float* D, int64_t B, i
     if (!x || !y || !D) return SDTW_ERR_INVALID_VALUE;
     if (mode != SDTW_DIST_EXACT) return SDTW_ERR_UNSUPPORTED;
     if (!dist_grid_ok(B, N, M)) return SDTW_ERR_UNSUPPORTED;
-    Carver c{static_cast<char*>(ws), ws_bytes};
+    (void)ws;
+    (void)ws_bytes;
     DistParams p{};
     p.x = x;
     p.y = y;
-    p.x2 = c.take<float>(B * N);
-    p.y2 = c.take<float>(B * M);
-    if (!c.ok) return SDTW_ERR_WORKSPACE;
     p.D = D;
     p.B = (int)B;
     p.N = (int)N;
@@ -258,9 +256,8 @@ int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const 
     p.cnt = c.take<int>(dist_bwd_counters(B, N, M, K));
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     if (mask) {
-        hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
-        if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
-        if (e != hipSuccess) return SDTW_ERR_LAUNCH;
+        if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess)
+            return SDTW_ERR_LAUNCH;
         p.x2 = x2;
         p.y2 = y2;
     }
@@ -313,9 +310,7 @@ int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int
     float* y2 = c.take<float>(B * M);
     const DPScratch d = carve_dp(c, B, N, M);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
-    hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
-    if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
-    if (e != hipSuccess) return SDTW_ERR_LAUNCH;
+    if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess) return SDTW_ERR_LAUNCH;
     DPParams p{};
     fill_dp(p, d, B, N, M, K, gamma, bandwidth);
     p.x = x;
@@ -332,9 +327,7 @@ static int fused_bwd_common(const float* x, const float* y, const float* R, cons
                             float* E, float* x2, float* y2, const DPScratch& d, int64_t B,
                             int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
                             hipStream_t st) {
-    hipError_t e = launch_norms(x, x2, B * N, (int)K, st);
-    if (e == hipSuccess) e = launch_norms(y, y2, B * M, (int)K, st);
-    if (e != hipSuccess) return SDTW_ERR_LAUNCH;
+    if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess) return SDTW_ERR_LAUNCH;
     DPParams p{};
     fill_dp(p, d, B, N, M, K, gamma, bandwidth);
     p.x = x;
@@ -369,8 +362,6 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
     DistBwdParams q{};
     q.x = x;
     q.y = y;
-    q.x2 = x2;
-    q.y2 = y2;
     q.D = nullptr;
     q.G = Ebuf;
     q.gx = gx;

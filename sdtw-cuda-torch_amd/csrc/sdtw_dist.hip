@@ -1,9 +1,11 @@
 // sdtw_dist.hip -- squared-Euclidean cost and its gradient for gfx950.
 //
-//   norms_kernel      x2[r] = sum_k x[r,k]^2 in ATen's CPU order (eight lanes per row).
+//   norms_kernel      x2[r] = sum_k x[r,k]^2 in ATen's CPU order (eight lanes per row), for
+//                     the fused recursions and the clamp mask of the backward.
 //   dist_kernel       D = clamp_min(x2 + y2 - 2 x.y^T, 0): 64x64 output tiles, x/y k-slices
 //                     staged in LDS, every output's dot product a sequential FMA chain over k
-//                     (the order of the host GEMM), so D has the reference's bits.
+//                     (the order of the host GEMM), so D has the reference's bits; the
+//                     tile's row norms are computed in the kernel (same bits as norms_kernel).
 //   dist_bwd_mfma_kernel
 //                     gx = 2 (x * rowsum(G') - G' y) and gy = 2 (y * colsum(G') - G'^T x)
 //                     on the matrix cores, with G' = G masked by the clamp (clamp_min
@@ -15,17 +17,12 @@
 
 namespace sdtw {
 
-// Eight threads per row: for K >= 8 thread t computes ATen's vector lane t (the scalar
-// row_sum over v[8c + t]); the row's first thread adds the tail and the eight lane sums in
-// ATen's order (aten_sumsq), so the result has the same bits with 8x the parallelism.
-__global__ void __launch_bounds__(256) norms_kernel(const float* __restrict__ v,
-                                                    float* __restrict__ out, int64_t rows,
-                                                    int K) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t r = gid >> 3;
-    const int t = (int)(gid & 7);
-    const bool ok = r < rows;
-    const float* row = v + (ok ? r : 0) * K;
+// Row norm with eight threads per row (threads 8g .. 8g + 7 of a wave share a row): for
+// K >= 8 thread t computes ATen's vector lane t (the scalar row_sum over v[8c + t]); the
+// row's first thread adds the tail and the eight lane sums in ATen's order (aten_sumsq), so
+// the result has the same bits with 8x the parallelism.  Every thread of the wave must
+// call it (the lane sums are exchanged with shuffles); the value is returned in thread t = 0.
+SDTW_DEV float row_norm8(const float* row, int K, int t, bool ok) {
     if (K >= 8) {
         const int nvec = K / 8;
         const float part = ok ? aten_row_sum_sq(row + t, 8, nvec) : 0.0f;
@@ -33,23 +30,42 @@ __global__ void __launch_bounds__(256) norms_kernel(const float* __restrict__ v,
         float lane[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) lane[j] = __shfl(part, base + j);
+        float fa = 0.0f;
         if (ok && t == 0) {
-            float fa = 0.0f;
             for (int e = nvec * 8; e < K; ++e) fa = __fadd_rn(fa, sq(row[e]));
 #pragma unroll
             for (int j = 0; j < 8; ++j) fa = __fadd_rn(fa, lane[j]);
-            out[r] = fa;
         }
-    } else if (ok && t == 0) {
-        out[r] = __fadd_rn(0.0f, aten_row_sum_sq(row, 1, K));
+        return fa;
     }
+    return (ok && t == 0) ? __fadd_rn(0.0f, aten_row_sum_sq(row, 1, K)) : 0.0f;
 }
 
-hipError_t launch_norms(const float* v, float* out, int64_t rows, int K, hipStream_t st) {
+// Norms of two row sets in one launch: rows [0, rows0) of v0 into out0, then rows0 more
+// of v1 into out1.
+__global__ void __launch_bounds__(256) norms_kernel(const float* __restrict__ v0,
+                                                    float* __restrict__ out0, int64_t rows0,
+                                                    const float* __restrict__ v1,
+                                                    float* __restrict__ out1, int64_t rows1,
+                                                    int K) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t r = gid >> 3;
+    const int t = (int)(gid & 7);
+    const bool first = r < rows0;
+    const int64_t rr = first ? r : r - rows0;
+    const bool ok = first || rr < rows1;
+    const float* row = (first ? v0 : v1) + (ok ? rr : 0) * K;
+    const float v = row_norm8(row, K, t, ok);
+    if (ok && t == 0) (first ? out0 : out1)[rr] = v;
+}
+
+hipError_t launch_norms(const float* x, float* x2, int64_t rows_x, const float* y, float* y2,
+                        int64_t rows_y, int K, hipStream_t st) {
+    const int64_t rows = rows_x + rows_y;
     if (rows <= 0) return hipSuccess;
     const int64_t blocks = (rows * 8 + 255) / 256;
-    hipLaunchKernelGGL(norms_kernel, dim3((unsigned)blocks), dim3(256), 0, st, v, out, rows,
-                       K);
+    hipLaunchKernelGGL(norms_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, x2, rows_x,
+                       y, y2, rows_y, K);
     return hipGetLastError();
 }
 
@@ -65,6 +81,7 @@ template <bool MULADD>
 __global__ void __launch_bounds__(256) dist_kernel(DistParams p) {
     __shared__ float xs[KC][DT + 1];
     __shared__ float ys[KC][DT + 1];
+    __shared__ float xn[DT], yn[DT];  // norms of the tile's rows of x and y
     // XCD-aware tile order (workgroups go to the 8 XCDs round-robin by linear id): the
     // tiles of one pair, which read the same rows of x and y, run on one XCD's L2
     const int gx = gridDim.x, gy = gridDim.y;
@@ -79,6 +96,18 @@ __global__ void __launch_bounds__(256) dist_kernel(DistParams p) {
     const int N = p.N, M = p.M, K = p.K;
     const float* xb = p.x + (int64_t)b * N * K;
     const float* yb = p.y + (int64_t)b * M * K;
+    // the 128 row norms the tile needs, eight threads per row (visible after the first
+    // barrier of the k loop)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int task = threadIdx.x + 256 * q;
+        const int rr = task >> 3, t = task & 7;
+        const bool isx = rr < DT;
+        const int row = isx ? i0 + rr : j0 + (rr - DT);
+        const bool ok = row < (isx ? N : M);
+        const float v = row_norm8((isx ? xb : yb) + (int64_t)(ok ? row : 0) * K, K, t, ok);
+        if (t == 0) (isx ? xn : yn)[rr & (DT - 1)] = v;
+    }
     float acc[4][4];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
@@ -113,27 +142,21 @@ __global__ void __launch_bounds__(256) dist_kernel(DistParams p) {
         }
         __syncthreads();
     }
-    const float* x2 = p.x2 + (int64_t)b * N;
-    const float* y2 = p.y2 + (int64_t)b * M;
     float* Db = p.D + (int64_t)b * N * M;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const int i = i0 + ty + 16 * m;
         if (i >= N) continue;
-        const float xi = x2[i];
+        const float xi = xn[ty + 16 * m];
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
             const int j = j0 + tx + 16 * n;
-            if (j < M) Db[(int64_t)i * M + j] = clamp0(exact_cost_pre(xi, y2[j], acc[m][n]));
+            if (j < M) Db[(int64_t)i * M + j] = clamp0(exact_cost_pre(xi, yn[tx + 16 * n], acc[m][n]));
         }
     }
 }
 
 hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t st) {
-    hipError_t e = launch_norms(p.x, p.x2, (int64_t)p.B * p.N, p.K, st);
-    if (e != hipSuccess) return e;
-    e = launch_norms(p.y, p.y2, (int64_t)p.B * p.M, p.K, st);
-    if (e != hipSuccess) return e;
     (void)mfma;
     dim3 grid((p.M + DT - 1) / DT, (p.N + DT - 1) / DT, p.B);
     if (muladd)

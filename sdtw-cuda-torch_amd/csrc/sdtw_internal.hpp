@@ -31,8 +31,6 @@ struct DPParams {
 struct DistParams {
     const float* x;  // (B,N,K)
     const float* y;  // (B,M,K)
-    float* x2;       // (B,N)
-    float* y2;       // (B,M)
     float* D;        // (B,N,M)
     int B, N, M, K;
 };
@@ -80,7 +78,8 @@ inline int64_t dist_bwd_counters(int64_t B, int64_t N, int64_t M, int64_t K) {
     return a > b ? a : b;
 }
 
-hipError_t launch_norms(const float* v, float* out, int64_t rows, int K, hipStream_t st);
+hipError_t launch_norms(const float* x, float* x2, int64_t rows_x, const float* y, float* y2,
+                        int64_t rows_y, int K, hipStream_t st);
 hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t st);
 hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st);
 // exact = the reference CPU arithmetic restated bit for bit; else hardware fp32 exp2/log2
