@@ -781,8 +781,10 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     }
 
     // One group: 16 reverse steps from q0.  INTERIOR: every lane is inside the table for all
-    // of them (a band with a band below it, columns M + 62 - q0 .. M - 16 - q0 within [0, M),
-    // no Sakoe-Chiba band), so no cell needs the padding row or the inactive masking.  The
+    // of them (a full band, columns M + 62 - q0 .. M - 16 - q0 within [0, M), no Sakoe-Chiba
+    // band), so no cell needs the inactive masking, and the padding row below the table (E 0,
+    // R -inf, D 0; lane 63 of a full last band) arrives as the ring padding that fetch_lds
+    // supplies where no band lies below: the corner (j = M) is outside such a group.  The
     // interior groups form one run of q0, walked by a loop of its own (three loops in
     // sequence rather than a branch per group, which would join the loop-carried registers
     // of two bodies).  Only with costs from the distance matrix: with a tile-computing cost
@@ -852,7 +854,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     };
     int q0 = 0;
     if constexpr (!BAND && std::is_same<Cost, CostD>::value) {
-        const bool has_interior = b + 1 < nb;
+        const bool has_interior = (b + 1) * WAVE <= N;
         const int q_in = has_interior ? WAVE : S;
         const int q_out = has_interior ? max(((M - U) / U + 1) * U, WAVE) : S;
         for (; q0 < q_in; q0 += U)

@@ -54,6 +54,8 @@ CASES = [
     (32, 512, 512, 64, 1.0, None),    # config 2 (headline)
     (2, 1300, 700, 3, 1.0, None),     # N > 1024: several row blocks
     (2, 700, 1300, 3, 0.3, 50.0),
+    (2, 192, 160, 5, 0.5, None),      # full last band with interior groups
+    (2, 64, 300, 4, 1.0, None),       # one full band, interior groups
 ]
 
 
