@@ -159,8 +159,8 @@ SDTW_DEV double fwd_cell_exact(double R0, double R1, double R2, float d, double 
     const bool a2 = !a0 && !(R1 == m);
     const double Ra = a0 ? R1 : R0;
     const double Rb = a2 ? R1 : R2;
-    const double ea = fm::exp_tab((m - Ra) * inv_gamma, T);
-    const double eb = fm::exp_tab((m - Rb) * inv_gamma, T);
+    const double ea = fm::exp_tab_abs((m - Ra) * inv_gamma, T);
+    const double eb = fm::exp_tab_abs((m - Rb) * inv_gamma, T);
     const double rsum = (ea + eb) + 1.0;
     return fma(-gamma, fm::log_tab_1to3(rsum, L), ((double)d + m) + nanfix);
 }
@@ -415,26 +415,30 @@ struct CostScalar {
 };
 
 // shared-memory layout of the DP kernels:
-//   [ticket, counters 256 B][exp / log tables 2560 B][handoff rings][cost rings]
-// W + 1 produced/consumed counter pairs, one per handoff ring
-constexpr int kTabBytes = (64 + 256) * 8;
+//   [ticket, counters 256 B][exp (/ log) tables][handoff rings][cost rings]
+// W + 1 produced/consumed counter pairs, one per handoff ring; the tables are the exp table
+// (fm::kExpTabN doubles, 2 KiB), then, in the forward only, the log table (2 fm::kLogTabN
+// doubles, 8 KiB)
+constexpr int kTabBytesFwd = (fm::kExpTabN + 2 * fm::kLogTabN) * 8;
+constexpr int kTabBytesBwd = fm::kExpTabN * 8;
 struct Smem {
     unsigned char* base;
     int W;
     size_t ring_bytes;  // handoff rings of all bands
+    int tab_bytes;      // kTabBytesFwd or kTabBytesBwd
     SDTW_DEV int* ticket() const { return reinterpret_cast<int*>(base); }
     SDTW_DEV int* prod() const { return reinterpret_cast<int*>(base) + 4; }
     SDTW_DEV int* cons() const { return reinterpret_cast<int*>(base) + 4 + (W + 1); }
     SDTW_DEV double* tables() const { return reinterpret_cast<double*>(base + 256); }
-    SDTW_DEV unsigned char* ring() const { return base + 256 + kTabBytes; }
+    SDTW_DEV unsigned char* ring() const { return base + 256 + tab_bytes; }
     SDTW_DEV float* cost_ring(int w) const {
-        return reinterpret_cast<float*>(base + 256 + kTabBytes + ring_bytes) + (size_t)w * WAVE * CS;
+        return reinterpret_cast<float*>(base + 256 + tab_bytes + ring_bytes) + (size_t)w * WAVE * CS;
     }
     // every thread of the workgroup, before the first barrier
     SDTW_DEV void load_tables() const {
         double* t = tables();
-        for (int e = threadIdx.x; e < 64 + 256; e += blockDim.x)
-            t[e] = e < 64 ? fm::kExp2Tab[e] : fm::kLogTab[e - 64];
+        for (int e = threadIdx.x; e < tab_bytes / 8; e += blockDim.x)
+            t[e] = e < fm::kExpTabN ? fm::kExp2Tab[e] : fm::kLogTab[e - fm::kExpTabN];
     }
 };
 
@@ -459,7 +463,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 
     double* lring = reinterpret_cast<double*>(sm.ring());
     const double* tabE = sm.tables();     // exp / log tables in LDS
-    const double* tabL = tabE + 64;
+    const double* tabL = tabE + fm::kExpTabN;
     float* cring = sm.cost_ring(w);
     const float* crow = cring + l * CS;  // my row of the cost ring
     // LDS ring k carries the input of band k of this workgroup: ring 0 is filled by the
@@ -622,7 +626,7 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
 template <class Cost, bool BAND, bool EXACT>
 __global__ void __launch_bounds__(320) fwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W)};
+    Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W), kTabBytesFwd};
     // wave-uniform values are moved to scalar registers so that the branches on band,
     // group and pair compile to scalar branches, not exec-masked regions
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -869,7 +873,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 template <class Cost, bool BAND, bool EXACT>
 __global__ void __launch_bounds__(320) bwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W)};
+    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W), kTabBytesBwd};
     // wave-uniform values are moved to scalar registers so that the branches on band,
     // group and pair compile to scalar branches, not exec-masked regions
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -898,7 +902,7 @@ hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st);
 
 inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
     const size_t ring = bwd ? ring_bytes_bwd(P.W) : ring_bytes_fwd(P.W);
-    return 256 + kTabBytes + ring + (size_t)P.W * WAVE * CS * sizeof(float);
+    return 256 + (bwd ? kTabBytesBwd : kTabBytesFwd) + ring + (size_t)P.W * WAVE * CS * sizeof(float);
 }
 
 template <class K>

@@ -23,7 +23,7 @@ using namespace sdtw::fm;
 int main() {
     std::mt19937_64 g(12345);
     std::uniform_real_distribution<double> u01(0.0, 1.0);
-    double emax = 0.0, lmax = 0.0;
+    double emax = 0.0, amax = 0.0, lmax = 0.0;
     for (int i = 0; i < 400000; ++i) {
         // exp arguments: -2^e * U[0,1), e in [0, 11]: the recursions pass (m - R) / gamma <= 0
         const double x = -std::ldexp(u01(g), (int)(g() % 12));
@@ -32,16 +32,21 @@ int main() {
             const double err = (double)fabsl(((long double)exp_tab(x, kExp2Tab) - ref) / ref);
             if (err > emax) emax = err;
         }
+        // the forward's variant: absolute accuracy (its result is added to 1)
+        const double aerr = (double)fabsl((long double)exp_tab_abs(x, kExp2Tab) - ref);
+        if (aerr > amax) amax = aerr;
         // log arguments: a soft-min's sum of exponentials, in [1, 3]
         const double s = 1.0 + 2.0 * u01(g);
         const double le = (double)fabsl((long double)log_tab_1to3(s, kLogTab) - logl((long double)s));
         if (le > lmax) lmax = le;
     }
-    std::printf("%.6e %.6e\n", emax, lmax);
+    std::printf("%.6e %.6e %.6e\n", emax, lmax, amax);
     std::printf("%a %a %a %a\n", exp_tab(0.0, kExp2Tab), exp_tab(-INFINITY, kExp2Tab),
                 log_tab_1to3(1.0, kLogTab), log_tab_1to3(3.0, kLogTab));
     std::printf("%d %d\n", (int)std::isnan(log_tab_1to3(NAN, kLogTab)),
                 (int)(exp_tab(-1e300, kExp2Tab) == 0.0));
+    std::printf("%a %a %d\n", exp_tab_abs(0.0, kExp2Tab), exp_tab_abs(-INFINITY, kExp2Tab),
+                (int)(exp_tab_abs(-1e300, kExp2Tab) == 0.0));
     return 0;
 }
 """
@@ -63,8 +68,9 @@ def harness_output():
 
 
 def test_exp_and_log_accuracy(harness_output):
-    emax, lmax = (float(v) for v in harness_output[0].split())
+    emax, lmax, amax = (float(v) for v in harness_output[0].split())
     assert emax < 4e-16, emax  # relative
+    assert amax < 4e-16, amax  # absolute (exp_tab_abs, the forward's)
     assert lmax < 4e-16, lmax  # absolute, |log s| <= 1.1
 
 
@@ -76,6 +82,8 @@ def test_special_values(harness_output):
     assert abs(l3 - 1.0986122886681098) < 4e-16
     nan_ok, tiny_ok = (int(v) for v in harness_output[2].split())
     assert nan_ok == 1 and tiny_ok == 1
+    a0, ainf, atiny = harness_output[3].split()
+    assert float.fromhex(a0) == 1.0 and float.fromhex(ainf) == 0.0 and int(atiny) == 1
 
 
 def test_tables_are_generated_from_the_committed_generator():
