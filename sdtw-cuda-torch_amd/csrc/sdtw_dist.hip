@@ -2,10 +2,13 @@
 //
 //   norms_kernel      x2[r] = sum_k x[r,k]^2 in ATen's CPU order (eight lanes per row), for
 //                     the fused recursions and the clamp mask of the backward.
-//   dist_kernel       D = clamp_min(x2 + y2 - 2 x.y^T, 0): 64x64 output tiles, x/y k-slices
-//                     staged in LDS, every output's dot product a sequential FMA chain over k
-//                     (the order of the host GEMM), so D has the reference's bits; the
-//                     tile's row norms are computed in the kernel (same bits as norms_kernel).
+//   dist_xs_kernel    D = clamp_min(x2 + y2 - 2 x.y^T, 0) for K <= 64: 64x64 output tiles,
+//                     64 rows of x stationary in LDS and y tiles streamed through two LDS
+//                     buffers; every output's dot product a sequential FMA chain over k (the
+//                     order of the host GEMM) on the matrix cores, so D has the reference's
+//                     bits; row norms computed from the staged tiles (norms_kernel's bits).
+//   dist_kernel       the same on the VALU with k chunks through LDS, for K > 64 and for the
+//                     tiny problems whose reference dot is ATen's multiply-then-add kernel.
 //   dist_bwd_mfma_kernel
 //                     gx = 2 (x * rowsum(G') - G' y) and gy = 2 (y * colsum(G') - G'^T x)
 //                     on the matrix cores, with G' = G masked by the clamp (clamp_min
@@ -156,13 +159,185 @@ __global__ void __launch_bounds__(256) dist_kernel(DistParams p) {
     }
 }
 
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------------------
+// Exact distance on the matrix cores, for K <= 64.  A chain of v_mfma_f32_16x16x4_f32 over
+// k = 0, 4, 8, ... from a zero accumulator computes each output as one sequential fp32 FMA
+// chain over k (measured bit-identical on gfx950; the fused cost tiles rely on the same
+// property), which is the order of the host GEMM, so D keeps the reference's bits.  Tiles
+// 64 (rows of x) x 64 (rows of y); wave w owns rows 16w .. 16w + 15 against the four
+// 16-column blocks (A operand x[16w + (l & 15)][k], B operand y[16nb + (l & 15)][k],
+// k = 4s + (l >> 4)).  x and y tiles sit in LDS row-major with a row stride of XS = 68
+// floats: the staging writes (consecutive k of a row) and the operand reads (16 rows at 4
+// consecutive k: banks 4 (row mod 16) + k mod 4) each cover 64 distinct banks.  Padding rows,
+// columns and features load as 0: fma(0, 0, acc) leaves a chain unchanged, and padding
+// outputs are not stored.  The row norms are computed from the staged tiles (norms_kernel's
+// arithmetic, so the same bits).
+// ---------------------------------------------------------------------------------------
+constexpr int KM = 64;
+constexpr int XS = 68;
+
+// ---------------------------------------------------------------------------------------
+// A workgroup owns 64 rows of x of one pair (x stationary) and walks a run of the pair's
+// 64-column tiles of y: the tiles are split into p.ysplit runs so that enough workgroups are
+// in flight to hide each other's latency.  The x tile and its norms are staged once; the
+// next y tile is loaded into registers while the matrix cores work on the current one, then
+// stored into the other of two LDS buffers and its norms computed from LDS.  VEC: K % 4 == 0,
+// rows are loaded as 16-byte vectors.
+// ---------------------------------------------------------------------------------------
+template <bool VEC>
+__global__ void __launch_bounds__(256) dist_xs_kernel(DistParams p) {
+    __shared__ __align__(16) float xs[DT * XS];
+    __shared__ __align__(16) float ys[2][DT * XS];
+    __shared__ float xn[DT], yn[2][DT];
+    // workgroup = (pair, row block); XCD-aware order: the row blocks of a pair, which read
+    // the same y, run on one XCD's L2
+    const int nrb = (p.N + DT - 1) / DT;
+    const int nwg = gridDim.x;
+    const int id = blockIdx.x;
+    const int v = (nwg & 7) == 0 ? (id & 7) * (nwg >> 3) + (id >> 3) : id;
+    const int ys_ = p.ysplit;
+    const int b = __builtin_amdgcn_readfirstlane(v / (nrb * ys_));
+    const int i0 = __builtin_amdgcn_readfirstlane(((v / ys_) % nrb) * DT);
+    const int part = __builtin_amdgcn_readfirstlane(v % ys_);
+    const int l = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int N = p.N, M = p.M, K = p.K;
+    const float* xb = p.x + (int64_t)b * N * K;
+    const float* ybase = p.y + (int64_t)b * M * K;
+    float* Db = p.D + (int64_t)b * N * M;
+    // staging of 64 rows x 64 features: VEC, thread t takes row 4q + (t >> 4), features
+    // 4 (t & 15) .. + 3 for q = 0..3; else element e = t + 256 q: row e / 64, feature e % 64
+    float4 pre[4];
+    auto load_tile = [&](const float* src, int r0, int rows) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (VEC) {
+                const int r = 16 * q + (threadIdx.x >> 4), k = 4 * (threadIdx.x & 15);
+                pre[q] = (r0 + r < rows && k < K)
+                             ? *reinterpret_cast<const float4*>(src + (int64_t)(r0 + r) * K + k)
+                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            } else {
+                float e4[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int e = threadIdx.x + 256 * (4 * q + c);
+                    const int r = e / KM, k = e % KM;
+                    e4[c] = (r0 + r < rows && k < K) ? src[(int64_t)(r0 + r) * K + k] : 0.0f;
+                }
+                pre[q] = make_float4(e4[0], e4[1], e4[2], e4[3]);
+            }
+        }
+    };
+    auto store_tile = [&](float* dst) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (VEC) {
+                const int r = 16 * q + (threadIdx.x >> 4), k = 4 * (threadIdx.x & 15);
+                *reinterpret_cast<float4*>(dst + r * XS + k) = pre[q];
+            } else {
+                const float e4[4] = {pre[q].x, pre[q].y, pre[q].z, pre[q].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int e = threadIdx.x + 256 * (4 * q + c);
+                    dst[(e / KM) * XS + e % KM] = e4[c];
+                }
+            }
+        }
+    };
+    // norms of the 64 staged rows (eight threads per row, ATen's order; padding rows give 0)
+    auto tile_norms = [&](const float* src, float* out) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int task = threadIdx.x + 256 * q;
+            const int r = task >> 3, t = task & 7;
+            const float nv = row_norm8(src + r * XS, K, t, true);
+            if (t == 0) out[r] = nv;
+        }
+    };
+    const int ntiles = (p.M + DT - 1) / DT;
+    const int per = (ntiles + ys_ - 1) / ys_;
+    const int jt0 = part * per, jt1 = min(ntiles, jt0 + per);
+    load_tile(xb, i0, N);
+    store_tile(xs);
+    load_tile(ybase, jt0 * DT, M);
+    store_tile(ys[0]);
+    __syncthreads();
+    tile_norms(xs, xn);
+    tile_norms(ys[0], yn[0]);
+    __syncthreads();
+    const float* xa = xs + (16 * w + (l & 15)) * XS + (l >> 4);
+    const int steps = (K + 3) / 4;
+    for (int jt = jt0; jt < jt1; ++jt) {
+        const int cur = (jt - jt0) & 1;
+        if (jt + 1 < jt1) load_tile(ybase, (jt + 1) * DT, M);
+        floatx4_t acc[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[nb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* yb0 = ys[cur] + (l & 15) * XS + (l >> 4);
+        auto kstep = [&](int s) {
+            const float a = xa[4 * s];
+            float bv[4];
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) bv[nb] = yb0[16 * nb * XS + 4 * s];
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv[nb], acc[nb], 0, 0, 0);
+        };
+        if (steps == KM / 4) {
+#pragma unroll
+            for (int s = 0; s < KM / 4; ++s) kstep(s);
+        } else {
+            for (int s = 0; s < steps; ++s) kstep(s);
+        }
+        // lane l holds rows 16w + 4 (l >> 4) + r of column 16nb + (l & 15)
+        const int j0 = jt * DT;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+            const int jl = 16 * nb + (l & 15);
+            const int j = j0 + jl;
+            const float y2 = yn[cur][jl];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int il = 16 * w + 4 * (l >> 4) + r;
+                const int i = i0 + il;
+                if (i < N && j < M) Db[(int64_t)i * M + j] = clamp0(exact_cost_pre(xn[il], y2, acc[nb][r]));
+            }
+        }
+        if (jt + 1 < jt1) {
+            store_tile(ys[cur ^ 1]);
+            __syncthreads();
+            tile_norms(ys[cur ^ 1], yn[cur ^ 1]);
+            __syncthreads();
+        }
+    }
+}
+
 hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t st) {
     (void)mfma;
-    dim3 grid((p.M + DT - 1) / DT, (p.N + DT - 1) / DT, p.B);
-    if (muladd)
+    if (muladd) {  // ATen's multiply-then-add kernel: not an FMA chain, so on the VALU
+        dim3 grid((p.M + DT - 1) / DT, (p.N + DT - 1) / DT, p.B);
         hipLaunchKernelGGL(dist_kernel<true>, grid, dim3(256), 0, st, p);
-    else
+    } else if (p.K <= KM) {
+        DistParams q = p;
+        const int64_t rows = (int64_t)p.B * ((p.N + DT - 1) / DT);
+        const int64_t ntiles = (p.M + DT - 1) / DT;
+        // about 2048 workgroups (at 3 resident per CU, latency is hidden; measured at the
+        // headline: 27 us against 33 us with one workgroup per row block), runs of at least
+        // one tile
+        int64_t split = (2048 + rows - 1) / rows;
+        split = split < 1 ? 1 : (split > ntiles ? ntiles : split);
+        q.ysplit = (int)split;
+        const int64_t wgs = rows * split;
+        if (p.K % 4 == 0)
+            hipLaunchKernelGGL(dist_xs_kernel<true>, dim3((unsigned)wgs), dim3(256), 0, st, q);
+        else
+            hipLaunchKernelGGL(dist_xs_kernel<false>, dim3((unsigned)wgs), dim3(256), 0, st, q);
+    } else {  // K > 64: chunks of k through LDS on the VALU
+        dim3 grid((p.M + DT - 1) / DT, (p.N + DT - 1) / DT, p.B);
         hipLaunchKernelGGL(dist_kernel<false>, grid, dim3(256), 0, st, p);
+    }
     return hipGetLastError();
 }
 
@@ -200,8 +375,6 @@ constexpr int GS_Y = 80;    // gy: LDS row stride of g
 constexpr int ZS = 80;      // LDS row stride of zs
 constexpr int GBUF = 64 * 80;  // floats per G' buffer (the larger layout)
 constexpr int ZBUF = 64 * ZS;  // floats per Z buffer
-
-typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 // Split reduction: z = b * ST + st (z after the XCD remap below); piece st takes chunks
 // [st*cps, (st+1)*cps).

@@ -33,6 +33,7 @@ struct DistParams {
     const float* y;  // (B,M,K)
     float* D;        // (B,N,M)
     int B, N, M, K;
+    int ysplit;      // runs of y tiles per row block (x-stationary kernel)
 };
 
 struct DistBwdParams {
