@@ -59,7 +59,8 @@ bool small_bmm(int64_t N, int64_t M, int64_t K) { return K * N * M < 400; }
 // distance-backward split-reduction scratch: partials, then counters
 size_t ws_dist_bwd(int64_t B, int64_t N, int64_t M, int64_t K) {
     return align_up(sizeof(float) * dist_bwd_split_floats(B, N, M, K)) +
-           align_up(sizeof(int) * dist_bwd_counters(B, N, M, K));
+           align_up(sizeof(int) * dist_bwd_counters(B, N, M, K)) +
+           align_up(sizeof(int) * dist_bwd_flags(B, N, M, K));
 }
 
 size_t ws_norms(int64_t B, int64_t N, int64_t M) {
@@ -254,6 +255,7 @@ int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const 
     float* y2 = c.take<float>(B * M);
     p.part = c.take<float>(dist_bwd_split_floats(B, N, M, K));
     p.cnt = c.take<int>(dist_bwd_counters(B, N, M, K));
+    p.flags = c.take<int>(dist_bwd_flags(B, N, M, K));
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     if (mask) {
         if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess)

@@ -426,17 +426,19 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
     // Two load paths, chosen per workgroup at compile time (a loop mixing them would make
     // the compiler wait for every load in flight): FG, every chunk a full 64 x 64 block of
     // rows of length M % 4 == 0, loaded as 16-byte vectors; else element by element with
-    // bounds.  ZF likewise for Z (K % 4 == 0 and K % KT == 0).  D is read only with MASK.
-    auto load_chunk = [&](int t0, Regs& R, auto fg_tag, auto zf_tag) {
+    // bounds.  ZF likewise for Z (K % 4 == 0 and K % KT == 0).  D is read only on the masked
+    // path (MK).
+    auto load_chunk = [&](int t0, Regs& R, auto fg_tag, auto zf_tag, auto mk_tag) {
         constexpr bool FG = decltype(fg_tag)::value, ZF = decltype(zf_tag)::value;
+        constexpr bool MK = MASK && decltype(mk_tag)::value;
         const int a0 = TRANS ? t0 : r0, b0 = TRANS ? r0 : t0;  // block origin in (N, M)
         if (FG) {
             const int64_t base = (int64_t)(a0 + (tid >> 4)) * M + b0 + 4 * (tid & 15);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 R.g[q] = *reinterpret_cast<const float4*>(Gb + base + (int64_t)16 * q * M);
-                R.d[q] = MASK ? *reinterpret_cast<const float4*>(Db + base + (int64_t)16 * q * M)
-                              : make_float4(1.f, 1.f, 1.f, 1.f);
+                R.d[q] = MK ? *reinterpret_cast<const float4*>(Db + base + (int64_t)16 * q * M)
+                            : make_float4(1.f, 1.f, 1.f, 1.f);
             }
         } else {
 #pragma unroll
@@ -453,7 +455,7 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
                     const int64_t idx = row + min(jb + v, M - 1);
                     const float gl = Gb[idx];
                     gv[v] = ok ? gl : 0.0f;
-                    if (MASK) {
+                    if (MK) {
                         const float dl = Db[idx];
                         dv[v] = ok ? dl : 1.0f;
                     } else {
@@ -488,13 +490,16 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
     };
     // Masked G' and Z into LDS buffer `buf`.  Cells whose clamped cost is positive pass the
     // clamp_min mask, NaN ones do not.  A cost of exactly 0 passes only where the pre-clamp
-    // value was >= 0: the first pass (EXACT false) masks such cells and records that it
-    // saw one, and a workgroup that saw one reruns with the exact per-cell check (loads of
-    // x and y rows inside the pipeline, hence slower).  Keeping loads out of the first pass
-    // lets the compiler wait on each chunk's loads alone.
-    bool zero_seen = false;
-    auto store_chunk = [&](int t0, const Regs& R, int buf, auto exact_tag) {
-        constexpr bool EXACT = MASK && decltype(exact_tag)::value;
+    // value was >= 0: the first run (EXACT false) masks every cost that is not positive and
+    // records that it saw one, and a workgroup that saw one reruns with the exact per-cell
+    // check (loads of x and y rows inside the pipeline, hence slower).  Keeping loads out of
+    // the first run lets the compiler wait on each chunk's loads alone.  The gx pass also
+    // publishes that record per workgroup (p.flags): where no cost was non-positive, the mask
+    // is the identity and the gy pass skips D.
+    bool nonpos_seen = false;
+    auto store_chunk = [&](int t0, const Regs& R, int buf, auto exact_tag, auto mk_tag) {
+        constexpr bool MK = MASK && decltype(mk_tag)::value;
+        constexpr bool EXACT = MK && decltype(exact_tag)::value;
         const int a0 = TRANS ? t0 : r0, b0 = TRANS ? r0 : t0;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -509,8 +514,8 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
                     if (!(d4[v] > 0.0f) &&  // positive passes (also the padding, d = 1)
                         !(d4[v] == 0.0f && i < N && j < M && clamp_passes<MULADD>(p, b, i, j)))
                         g4[v] = 0.0f;
-                } else {  // selects only: no branch, no load
-                    zero_seen |= d4[v] == 0.0f && i < N && j < M;
+                } else if (MK) {  // selects only: no branch, no load
+                    nonpos_seen |= !(d4[v] > 0.0f) && i < N && j < M;
                     g4[v] = d4[v] > 0.0f ? g4[v] : 0.0f;
                 }
             }
@@ -569,53 +574,67 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
     // state loads unconditionally (a register set conditionally reloaded inside the loop
     // would be copied between iterations, and a copy waits for every load in flight); the
     // last two to three chunks are an explicit epilogue.
-    auto run = [&](auto exact_tag, auto fg, auto zf) {
+    auto run = [&](auto exact_tag, auto fg, auto zf, auto mk) {
         Regs ra, rb;
-        if (nchunks > 0) load_chunk(cbeg * BT, ra, fg, zf);
-        if (nchunks > 1) load_chunk((cbeg + 1) * BT, rb, fg, zf);
+        if (nchunks > 0) load_chunk(cbeg * BT, ra, fg, zf, mk);
+        if (nchunks > 1) load_chunk((cbeg + 1) * BT, rb, fg, zf, mk);
         int c = 0;
         for (; c + 3 < nchunks; c += 2) {
-            store_chunk((cbeg + c) * BT, ra, 0, exact_tag);
-            load_chunk((cbeg + c + 2) * BT, ra, fg, zf);
+            store_chunk((cbeg + c) * BT, ra, 0, exact_tag, mk);
+            load_chunk((cbeg + c + 2) * BT, ra, fg, zf, mk);
             __syncthreads();
             multiply(0);
-            store_chunk((cbeg + c + 1) * BT, rb, 1, exact_tag);
-            load_chunk((cbeg + c + 3) * BT, rb, fg, zf);
+            store_chunk((cbeg + c + 1) * BT, rb, 1, exact_tag, mk);
+            load_chunk((cbeg + c + 3) * BT, rb, fg, zf, mk);
             __syncthreads();
             multiply(1);
         }
         const int rem = nchunks - c;  // 0 .. 3
         if (rem >= 1) {
-            store_chunk((cbeg + c) * BT, ra, 0, exact_tag);
-            if (rem == 3) load_chunk((cbeg + c + 2) * BT, ra, fg, zf);
+            store_chunk((cbeg + c) * BT, ra, 0, exact_tag, mk);
+            if (rem == 3) load_chunk((cbeg + c + 2) * BT, ra, fg, zf, mk);
             __syncthreads();
             multiply(0);
         }
         if (rem >= 2) {
-            store_chunk((cbeg + c + 1) * BT, rb, 1, exact_tag);
+            store_chunk((cbeg + c + 1) * BT, rb, 1, exact_tag, mk);
             __syncthreads();
             multiply(1);
         }
         if (rem == 3) {
-            store_chunk((cbeg + c + 2) * BT, ra, 0, exact_tag);
+            store_chunk((cbeg + c + 2) * BT, ra, 0, exact_tag, mk);
             __syncthreads();
             multiply(0);
         }
     };
     const bool fg = vec_g && r0 + 64 <= R_ && T_ % BT == 0;
     const bool zf = vec_z && K % KT == 0 && T_ % BT == 0;
-    auto run_any = [&](auto exact_tag) {
-        if (fg && zf) run(exact_tag, std::true_type{}, std::true_type{});
-        else if (fg) run(exact_tag, std::true_type{}, std::false_type{});
-        else run(exact_tag, std::false_type{}, std::false_type{});
+    auto run_any = [&](auto exact_tag, auto mk) {
+        if (fg && zf) run(exact_tag, std::true_type{}, std::true_type{}, mk);
+        else if (fg) run(exact_tag, std::true_type{}, std::false_type{}, mk);
+        else run(exact_tag, std::false_type{}, std::false_type{}, mk);
     };
-    run_any(std::false_type{});
-    if (MASK && __syncthreads_or(zero_seen)) {  // rare: rerun the tile with the exact mask
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) acc[kb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        rs_part = 0.0f;
-        run_any(std::true_type{});
+    // the gy pass: the mask is needed only if the gx pass saw a cost that was not positive
+    bool use_mask = MASK;
+    if (MASK && TRANS && p.flags) {
+        int any = 0;
+        for (int f = tid; f < p.nflags; f += 256) any |= p.flags[f];
+        use_mask = __syncthreads_or(any);
     }
+    int nonpos = 0;
+    if (use_mask) {
+        run_any(std::false_type{}, std::true_type{});
+        nonpos = __syncthreads_or(nonpos_seen);
+        if (nonpos) {  // rare: rerun the tile with the exact mask
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) acc[kb] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            rs_part = 0.0f;
+            run_any(std::true_type{}, std::true_type{});
+        }
+    } else {
+        run_any(std::false_type{}, std::false_type{});
+    }
+    if (MASK && !TRANS && p.flags && tid == 0) p.flags[id] = nonpos;
 
     // rs of row 16w + x: sum of the four lanes with (l & 15) == x
     float rs = rs_part + __shfl_xor(rs_part, 16);
@@ -709,12 +728,16 @@ hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st) {
         const int blocks = (int)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
         hipLaunchKernelGGL(zero_ints_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, st, p.cnt, n);
     }
-    if (p.muladd) {
-        launch_dist_bwd_one<false, true>(p, st);
-        launch_dist_bwd_one<true, true>(p, st);
+    // with the mask, the gx pass writes one flag per workgroup, which the gy pass reads
+    DistBwdParams q = p;
+    if (!q.mask) q.flags = nullptr;
+    q.nflags = (int)(dist_bwd_tiles(p.B, p.N, p.K) * (p.part ? dist_bwd_splits(p.B, p.N, p.M, p.K) : 1));
+    if (q.muladd) {
+        launch_dist_bwd_one<false, true>(q, st);
+        launch_dist_bwd_one<true, true>(q, st);
     } else {
-        launch_dist_bwd_one<false, false>(p, st);
-        launch_dist_bwd_one<true, false>(p, st);
+        launch_dist_bwd_one<false, false>(q, st);
+        launch_dist_bwd_one<true, false>(q, st);
     }
     return hipGetLastError();
 }

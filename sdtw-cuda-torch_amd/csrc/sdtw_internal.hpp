@@ -50,6 +50,8 @@ struct DistBwdParams {
     int muladd;
     float* part;      // split-reduction partials (dist_bwd_split_floats) or nullptr
     int* cnt;         // per-tile arrival counters (dist_bwd_tiles ints), or nullptr
+    int* flags;       // mask: per gx-pass workgroup "a cost was not positive" (dist_bwd_flags)
+    int nflags;
 };
 
 // Split reduction of the distance backward: the reduction of a 64-row x KT-feature output
@@ -77,6 +79,10 @@ inline int64_t dist_bwd_split_floats(int64_t B, int64_t N, int64_t M, int64_t K)
 inline int64_t dist_bwd_counters(int64_t B, int64_t N, int64_t M, int64_t K) {
     const int64_t a = dist_bwd_tiles(B, N, K), b = dist_bwd_tiles(B, M, K);
     return a > b ? a : b;
+}
+// workgroups of the gx pass (tiles times reduction pieces), one flag each
+inline int64_t dist_bwd_flags(int64_t B, int64_t N, int64_t M, int64_t K) {
+    return dist_bwd_tiles(B, N, K) * dist_bwd_splits(B, N, M, K);
 }
 
 hipError_t launch_norms(const float* x, float* x2, int64_t rows_x, const float* y, float* y2,
