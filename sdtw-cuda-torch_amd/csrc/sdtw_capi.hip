@@ -56,6 +56,11 @@ bool gamma_ok(double gamma) { return gamma > 0.0 && isfinite(gamma); }
 // ATen's naive bmm kernel (multiply, then add) runs when K*N*M < 400.
 bool small_bmm(int64_t N, int64_t M, int64_t K) { return K * N * M < 400; }
 
+// Bands per workgroup of the fused recursions: 2 where a producer wave per band computes the
+// matrix-core cost tiles (it needs a SIMD of its own: the fp32 matrix instructions take the
+// cycles of the SIMD they run on), else 4.
+int fused_wmax(int64_t N, int64_t M, int64_t K) { return (!small_bmm(N, M, K) && K <= 64) ? 2 : 4; }
+
 // distance-backward split-reduction scratch: partials, then counters
 size_t ws_dist_bwd(int64_t B, int64_t N, int64_t M, int64_t K) {
     return align_up(sizeof(float) * dist_bwd_split_floats(B, N, M, K)) +
@@ -69,8 +74,8 @@ size_t ws_norms(int64_t B, int64_t N, int64_t M) {
 
 // Wavefront-kernel scratch: [ticket, error flag][per-boundary rows].  The rows hold fp64
 // values (forward) or (E, R, D, tag) float4 (backward): 16 bytes per column.
-size_t ws_dp(int64_t B, int64_t N, int64_t M) {
-    const DPGeom g = dp_geom(N);
+size_t ws_dp(int64_t B, int64_t N, int64_t M, int wmax = 4) {
+    const DPGeom g = dp_geom(N, wmax);
     return 256 + align_up((size_t)16 * B * g.G * dp_row_entries(M));
 }
 
@@ -80,8 +85,8 @@ struct DPScratch {
     void* gring;
 };
 
-DPScratch carve_dp(Carver& c, int64_t B, int64_t N, int64_t M) {
-    const DPGeom g = dp_geom(N);
+DPScratch carve_dp(Carver& c, int64_t B, int64_t N, int64_t M, int wmax = 4) {
+    const DPGeom g = dp_geom(N, wmax);
     DPScratch d{};
     int* hdr = c.take<int>(64);
     d.gring = c.take<unsigned char>((size_t)16 * B * g.G * dp_row_entries(M));
@@ -93,8 +98,8 @@ DPScratch carve_dp(Carver& c, int64_t B, int64_t N, int64_t M) {
 }
 
 void fill_dp(DPParams& p, const DPScratch& d, int64_t B, int64_t N, int64_t M, int64_t K,
-             double gamma, double bandwidth) {
-    const DPGeom g = dp_geom(N);
+             double gamma, double bandwidth, int wmax = 4) {
+    const DPGeom g = dp_geom(N, wmax);
     p.ticket = d.ticket;
     p.err = d.err;
     p.gring = static_cast<double*>(d.gring);
@@ -199,9 +204,9 @@ size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) 
         case SDTW_OP_BWD:
             return ws_dp(B, N, M);
         case SDTW_OP_FUSED_FWD:
-            return ws_norms(B, N, M) + ws_dp(B, N, M);
+            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_wmax(N, M, K));
         case SDTW_OP_FUSED_BWD:
-            return ws_norms(B, N, M) + ws_dp(B, N, M) + align_up(sizeof(float) * B * N * M) +
+            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_wmax(N, M, K)) + align_up(sizeof(float) * B * N * M) +
                    ws_dist_bwd(B, N, M, K);
         default:
             return 0;
@@ -310,11 +315,12 @@ int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const DPScratch d = carve_dp(c, B, N, M);
+    const int wmax = fused_wmax(N, M, K);
+    const DPScratch d = carve_dp(c, B, N, M, wmax);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess) return SDTW_ERR_LAUNCH;
     DPParams p{};
-    fill_dp(p, d, B, N, M, K, gamma, bandwidth);
+    fill_dp(p, d, B, N, M, K, gamma, bandwidth, wmax);
     p.x = x;
     p.y = y;
     p.x2 = x2;
@@ -331,7 +337,7 @@ static int fused_bwd_common(const float* x, const float* y, const float* R, cons
                             hipStream_t st) {
     if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess) return SDTW_ERR_LAUNCH;
     DPParams p{};
-    fill_dp(p, d, B, N, M, K, gamma, bandwidth);
+    fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_wmax(N, M, K));
     p.x = x;
     p.y = y;
     p.x2 = x2;
@@ -354,7 +360,7 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const DPScratch d = carve_dp(c, B, N, M);
+    const DPScratch d = carve_dp(c, B, N, M, fused_wmax(N, M, K));
     float* Ebuf = c.take<float>(B * N * M);
     float* part = c.take<float>(dist_bwd_split_floats(B, N, M, K));
     int* cnt = c.take<int>(dist_bwd_counters(B, N, M, K));
@@ -388,7 +394,7 @@ int sdtw_fused_bwd_e_f32(const float* x, const float* y, const float* R, const f
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const DPScratch d = carve_dp(c, B, N, M);
+    const DPScratch d = carve_dp(c, B, N, M, fused_wmax(N, M, K));
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     return fused_bwd_common(x, y, R, gout, E, x2, y2, d, B, N, M, K, gamma, bandwidth,
                             (hipStream_t)stream);

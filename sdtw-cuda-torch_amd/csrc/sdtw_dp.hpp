@@ -289,6 +289,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <int KX>
 struct CostMfma {
+    static constexpr int KXV = KX;
     static constexpr int NKK = KX / 4;
     const float* y;
     const float* y2;
@@ -414,6 +415,46 @@ struct CostScalar {
     }
 };
 
+// Matrix-core costs computed by a producer wave (one per band, sharing the SIMD with the
+// band's compute wave, so the matrix pipe runs beside the recursion's VALU chain instead of
+// inside its instruction stream).  The producer writes the tiles into the band's cost ring
+// in reading order (tile t: columns 16t.. in the forward, M - 16 (t + 1).. in the backward,
+// CostMfma's arithmetic and layout) and counts them in ready[w]; the compute wave counts its
+// finished groups in done[w].  The compute wave starts group g once tiles 0 .. g + 1 are in
+// (its cost reads during group g reach tile g + 1).  The producer stores tile t once the
+// slots it reuses (those of the columns 128 further on in reading order) are dead: in the
+// forward they are last read in group t - 5, so done >= t - 4; in the backward they also
+// carry g*E until the flush at the end of group t - 4, and done is counted before the flush,
+// so done >= t - 2.  Both leave the producer at least one group of slack, and neither wait
+// can close a cycle.  Waits are bounded like every other (timeout flag).
+struct Smem;
+
+template <class C>
+struct Produced : std::false_type {};
+template <int KX>
+struct Produced<CostMfma<KX>> : std::true_type {};
+
+struct CostRing {
+    const int* ready;
+    int* done;
+    int* err;
+    int known, groups, pro;
+    SDTW_DEV void bind(const Smem& sm, int w, int* e);
+    SDTW_DEV void init(const DPParams&, int, int) {}
+    SDTW_DEV void wait(int n) {
+        if (!wait_at_least(ready, n, known, err)) known = 1 << 30;  // timed out: flag raised
+    }
+    // the two prologue tiles
+    SDTW_DEV void prologue(float*, int) { wait(++pro); }
+    SDTW_DEV void preload(int) {}
+    SDTW_DEV void begin(float*, int) { wait(groups + 2); }
+    SDTW_DEV void step(int, int, int) {}
+    SDTW_DEV void end(float*, int, int) {
+        ++groups;
+        if ((threadIdx.x & (WAVE - 1)) == 0) lds_publish(done, groups);
+    }
+};
+
 // shared-memory layout of the DP kernels:
 //   [ticket, counters 256 B][exp (/ log) tables][handoff rings][cost rings]
 // W + 1 produced/consumed counter pairs, one per handoff ring; the tables are the exp table
@@ -429,6 +470,10 @@ struct Smem {
     SDTW_DEV int* ticket() const { return reinterpret_cast<int*>(base); }
     SDTW_DEV int* prod() const { return reinterpret_cast<int*>(base) + 4; }
     SDTW_DEV int* cons() const { return reinterpret_cast<int*>(base) + 4 + (W + 1); }
+    // matrix-core costs from producer waves: tiles finished per band, groups finished by the
+    // band's compute wave (8 + 8 ints from int 16 of the header)
+    SDTW_DEV int* ready() const { return reinterpret_cast<int*>(base) + 16; }
+    SDTW_DEV int* done() const { return reinterpret_cast<int*>(base) + 24; }
     SDTW_DEV double* tables() const { return reinterpret_cast<double*>(base + 256); }
     SDTW_DEV unsigned char* ring() const { return base + 256 + tab_bytes; }
     SDTW_DEV float* cost_ring(int w) const {
@@ -441,6 +486,41 @@ struct Smem {
             t[e] = e < fm::kExpTabN ? fm::kExp2Tab[e] : fm::kLogTab[e - fm::kExpTabN];
     }
 };
+
+SDTW_DEV void CostRing::bind(const Smem& sm, int w, int* e) {
+    ready = sm.ready() + w;
+    done = sm.done() + w;
+    err = e;
+    known = 0;
+    groups = 0;
+    pro = 0;
+}
+
+// The producer wave of band b (compute wave w): tile t of the pair's cost in reading order,
+// products issued before the wait for the ring slots, the next tile's B operand loaded
+// right after the store.
+template <int KX, bool BWD>
+SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int w) {
+    CostMfma<KX> c;
+    c.init(P, p, b);
+    float* ring = sm.cost_ring(w);
+    const int* done = sm.done() + w;
+    int* ready = sm.ready() + w;
+    int known = 0;
+    const int T = P.S / U + 1;  // tiles the compute wave reads
+    auto col = [&](int t) { return BWD ? P.M - TC * (t + 1) : TC * t; };
+    c.issue(col(0));
+    for (int t = 0; t < T; ++t) {
+        c.zero();
+#pragma unroll
+        for (int kk = 0; kk < CostMfma<KX>::NKK; ++kk) c.mma(kk);
+        const int need = BWD ? t - 2 : t - 4;
+        if (need > 0 && !wait_at_least(done, need, known, P.err)) return;
+        c.finish(ring, col(t));
+        if (t + 1 < T) c.issue(col(t + 1));
+        if ((threadIdx.x & (WAVE - 1)) == 0) lds_publish(ready, t + 1);
+    }
+}
 
 // W + 1 handoff rings: one per band plus the helper wave's
 SDTW_HD size_t ring_bytes_fwd(int W) { return (size_t)(W + 1) * RS * sizeof(double); }
@@ -623,8 +703,13 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
     }
 }
 
+// Waves of a workgroup: compute waves 0 .. W-1 (one band each) and the helper wave W; with
+// matrix-core costs (W <= 2), the producer waves W .. 2W-1 (of bands 0 .. W-1, on the SIMDs
+// the compute waves leave free when waves are placed round-robin) and the helper wave 2W.
+constexpr int kDPThreads = 5 * WAVE;
+
 template <class Cost, bool BAND, bool EXACT>
-__global__ void __launch_bounds__(320) fwd_kernel(DPParams P) {
+__global__ void __launch_bounds__(kDPThreads) fwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W), kTabBytesFwd};
     // wave-uniform values are moved to scalar registers so that the branches on band,
@@ -632,6 +717,7 @@ __global__ void __launch_bounds__(320) fwd_kernel(DPParams P) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;  // prod and cons are contiguous
+    if (threadIdx.x < 16) sm.ready()[threadIdx.x] = 0;            // ready and done likewise
     sm.load_tables();
     // ring 0 starts at +inf: the padding row above band 0 (the helper wave overwrites it
     // in workgroups that have a band above them)
@@ -639,14 +725,27 @@ __global__ void __launch_bounds__(320) fwd_kernel(DPParams P) {
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G, g = t - p * P.G;
-    if (w == P.W) {  // helper wave: the previous workgroup's last row into ring 0
+    if (w == (Produced<Cost>::value ? 2 * P.W : P.W)) {
+        // helper wave: the previous workgroup's last row into ring 0
         if (g > 0) helper_wave(P, sm, P.gring + ((int64_t)p * P.G + (g - 1)) * P.RW + RPAD, 0);
         return;
     }
-    if (g * P.W + w >= P.nb) return;
-    Cost cost;
-    cost.init(P, p, g * P.W + w);
-    fwd_band<Cost, BAND, EXACT>(P, cost, sm, p, g, w);
+    if constexpr (Produced<Cost>::value) {
+        const int wb = w >= P.W ? w - P.W : w;  // band of this compute or producer wave
+        if (g * P.W + wb >= P.nb) return;
+        if (w >= P.W) {
+            producer_wave<Cost::KXV, false>(P, sm, p, g * P.W + wb, wb);
+        } else {
+            CostRing cost;
+            cost.bind(sm, w, P.err);
+            fwd_band<CostRing, BAND, EXACT>(P, cost, sm, p, g, w);
+        }
+    } else {
+        if (g * P.W + w >= P.nb) return;
+        Cost cost;
+        cost.init(P, p, g * P.W + w);
+        fwd_band<Cost, BAND, EXACT>(P, cost, sm, p, g, w);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -857,7 +956,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         return true;
     };
     int q0 = 0;
-    if constexpr (!BAND && std::is_same<Cost, CostD>::value) {
+    if constexpr (!BAND && (std::is_same<Cost, CostD>::value || std::is_same<Cost, CostRing>::value)) {
         const bool has_interior = (b + 1) * WAVE <= N;
         const int q_in = has_interior ? WAVE : S;
         const int q_out = has_interior ? max(((M - U) / U + 1) * U, WAVE) : S;
@@ -871,7 +970,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 }
 
 template <class Cost, bool BAND, bool EXACT>
-__global__ void __launch_bounds__(320) bwd_kernel(DPParams P) {
+__global__ void __launch_bounds__(kDPThreads) bwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W), kTabBytesBwd};
     // wave-uniform values are moved to scalar registers so that the branches on band,
@@ -879,19 +978,33 @@ __global__ void __launch_bounds__(320) bwd_kernel(DPParams P) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;
+    if (threadIdx.x < 16) sm.ready()[threadIdx.x] = 0;
     sm.load_tables();
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G;
     const int g = (P.G - 1) - (t - p * P.G);  // lowest ticket of a pair takes the bottom group
-    if (w == P.W) {  // helper wave: the next workgroup's first row into ring W
+    if (w == (Produced<Cost>::value ? 2 * P.W : P.W)) {
+        // helper wave: the next workgroup's first row into ring W
         if (g + 1 < P.G) helper_wave(P, sm, P.gring4 + ((int64_t)p * P.G + (g + 1)) * P.RW + RPAD, P.W);
         return;
     }
-    if (g * P.W + w >= P.nb) return;
-    Cost cost;
-    cost.init(P, p, g * P.W + w);
-    bwd_band<Cost, BAND, EXACT>(P, cost, sm, p, g, w);
+    if constexpr (Produced<Cost>::value) {
+        const int wb = w >= P.W ? w - P.W : w;
+        if (g * P.W + wb >= P.nb) return;
+        if (w >= P.W) {
+            producer_wave<Cost::KXV, true>(P, sm, p, g * P.W + wb, wb);
+        } else {
+            CostRing cost;
+            cost.bind(sm, w, P.err);
+            bwd_band<CostRing, BAND, EXACT>(P, cost, sm, p, g, w);
+        }
+    } else {
+        if (g * P.W + w >= P.nb) return;
+        Cost cost;
+        cost.init(P, p, g * P.W + w);
+        bwd_band<Cost, BAND, EXACT>(P, cost, sm, p, g, w);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -906,7 +1019,7 @@ inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
 }
 
 template <class K>
-hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, hipStream_t st) {
+hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipStream_t st) {
     const size_t lds = dp_smem_bytes(P, bwd);
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -915,8 +1028,9 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, hipStream_t st) {
     }
     hipError_t e = launch_dp_prep(P, bwd, st);
     if (e != hipSuccess) return e;
-    // one wave per band, plus a helper wave when a pair spans several workgroups
-    const int waves = P.W + (P.G > 1 ? 1 : 0);
+    // one wave per band, plus a helper wave when a pair spans several workgroups; with
+    // matrix-core costs, the helper slot and one producer wave per band
+    const int waves = produced ? 2 * P.W + 1 : P.W + (P.G > 1 ? 1 : 0);
     hipLaunchKernelGGL(kernel, dim3(P.B * P.G), dim3(waves * WAVE), lds, st, P);
     return hipGetLastError();
 }
@@ -924,11 +1038,11 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, hipStream_t st) {
 template <class Cost, bool BWD, bool EXACT>
 hipError_t launch_cost(const DPParams& P, hipStream_t st) {
     if constexpr (BWD) {
-        if (P.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT>, P, true, st);
-        return launch_dp(bwd_kernel<Cost, false, EXACT>, P, true, st);
+        if (P.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT>, P, true, Produced<Cost>::value, st);
+        return launch_dp(bwd_kernel<Cost, false, EXACT>, P, true, Produced<Cost>::value, st);
     } else {
-        if (P.bw > 0.0) return launch_dp(fwd_kernel<Cost, true, EXACT>, P, false, st);
-        return launch_dp(fwd_kernel<Cost, false, EXACT>, P, false, st);
+        if (P.bw > 0.0) return launch_dp(fwd_kernel<Cost, true, EXACT>, P, false, Produced<Cost>::value, st);
+        return launch_dp(fwd_kernel<Cost, false, EXACT>, P, false, Produced<Cost>::value, st);
     }
 }
 

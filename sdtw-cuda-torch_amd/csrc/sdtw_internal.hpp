@@ -100,10 +100,12 @@ hipError_t launch_table_pack(const float* Rd, float* Rt, int B, int N, int M, hi
 struct DPGeom {
     int nb, W, G;
 };
-inline DPGeom dp_geom(int64_t N) {
+// wmax: bands per workgroup (4, one compute wave per SIMD; 2 with producer waves, which take
+// the other two SIMDs)
+inline DPGeom dp_geom(int64_t N, int wmax = 4) {
     DPGeom g;
     g.nb = (int)((N + 63) / 64);
-    g.W = g.nb < 4 ? g.nb : 4;
+    g.W = g.nb < wmax ? g.nb : wmax;
     g.G = (g.nb + g.W - 1) / g.W;
     return g;
 }
