@@ -415,24 +415,30 @@ struct CostScalar {
     }
 };
 
-// Matrix-core costs computed by a producer wave (one per band, sharing the SIMD with the
-// band's compute wave, so the matrix pipe runs beside the recursion's VALU chain instead of
-// inside its instruction stream).  The producer writes the tiles into the band's cost ring
-// in reading order (tile t: columns 16t.. in the forward, M - 16 (t + 1).. in the backward,
-// CostMfma's arithmetic and layout) and counts them in ready[w]; the compute wave counts its
-// finished groups in done[w].  The compute wave starts group g once tiles 0 .. g + 1 are in
-// (its cost reads during group g reach tile g + 1).  The producer stores tile t once the
-// slots it reuses (those of the columns 128 further on in reading order) are dead: in the
-// forward they are last read in group t - 5, so done >= t - 4; in the backward they also
-// carry g*E until the flush at the end of group t - 4, and done is counted before the flush,
-// so done >= t - 2.  Both leave the producer at least one group of slack, and neither wait
-// can close a cycle.  Waits are bounded like every other (timeout flag).
+// Costs staged by a producer wave, one per band: matrix-core tiles (CostMfma; the producer
+// then needs a SIMD of its own, since the fp32 matrix instructions take the cycles of the
+// SIMD they run on) or, in the backward, tiles loaded from D (CostD; light enough to share
+// the compute wave's SIMD).  The producer writes the tiles into the band's cost ring in reading order (tile t:
+// columns 16t.. in the forward, M - 16 (t + 1).. in the backward, in the provider's layout)
+// and counts them in ready[w]; the compute wave counts its finished groups in done[w].  The
+// compute wave starts group g once tiles 0 .. g + 1 are in (its cost reads during group g
+// reach tile g + 1).  The producer stores tile t once the slots it reuses (those of the
+// columns 128 further on in reading order) are dead: in the forward they are last read in
+// group t - 5, so done >= t - 4; in the backward they also carry g*E until group t - 4 has
+// finished, whose G tile the producer itself then reads (GTile) before reusing the
+// slots, so done >= t - 3.  Both leave the producer at least two groups of slack, and
+// neither wait can close a cycle.  Waits are bounded like every other (timeout flag).
 struct Smem;
 
-template <class C>
+// whether the costs of a recursion come from producer waves: matrix-core tiles in both
+// directions; D tiles in the backward only (in the forward the compute wave's own loads cost
+// less than the ring handshake)
+template <class C, bool BWD>
 struct Produced : std::false_type {};
-template <int KX>
-struct Produced<CostMfma<KX>> : std::true_type {};
+template <int KX, bool BWD>
+struct Produced<CostMfma<KX>, BWD> : std::true_type {};
+template <>
+struct Produced<CostD, true> : std::true_type {};
 
 struct CostRing {
     const int* ready;
@@ -496,29 +502,89 @@ SDTW_DEV void CostRing::bind(const Smem& sm, int w, int* e) {
     pro = 0;
 }
 
-// The producer wave of band b (compute wave w): tile t of the pair's cost in reading order,
-// products issued before the wait for the ring slots, the next tile's B operand loaded
-// right after the store.
-template <int KX, bool BWD>
+// The G tile completed by the backward group at q0 of band b: columns [M + 47 - q0,
+// M + 63 - q0) of every row (each step writes g*E into the cost-ring slot of the cost it has
+// just consumed).  read() takes it from the band's cost ring (lane l: column c0 + (l & 15),
+// rows 4k + (l >> 4)), write() stores it as 16 coalesced 4-row blocks; a producer wave puts
+// its next loads between the two, so they do not queue behind the stores.
+struct GTile {
+    float v[16];
+    int col;  // this lane's column, or -1
+    SDTW_DEV void read(const DPParams& P, const float* cring, int q0) {
+        const int l = threadIdx.x & (WAVE - 1);
+        col = P.M + 47 - q0 + (l & 15);
+        if ((unsigned)col >= (unsigned)P.M) {
+            col = -1;
+            return;
+        }
+        const float* src = cring + (l >> 4) * CS + (col & (CR - 1));
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = src[4 * k * CS];
+    }
+    SDTW_DEV void write(const DPParams& P, int p, int b) const {
+        if (col < 0) return;
+        const int l = threadIdx.x & (WAVE - 1);
+        const int M = P.M;
+        const int nrows = min(P.N - b * WAVE, WAVE);
+        float* dst = P.G_out + ((int64_t)p * P.N + b * WAVE + (l >> 4)) * M + col;
+        if (nrows == WAVE) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                *dst = v[k];
+                dst += 4 * M;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                if (4 * k + (l >> 4) < nrows) *dst = v[k];
+                dst += 4 * M;
+            }
+        }
+    }
+};
+
+// The producer wave of band b (compute wave w): tile t of the pair's cost in reading order;
+// matrix-core products are issued before the wait for the ring slots, the next tile's loads
+// (its B operand, or its D values) right after the store.  In the backward the G tile of
+// group t - 4 is read from the slots before they are reused and stored after those loads;
+// the last groups' tiles are stored after the loop.
+template <class Src, bool BWD>
 SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int w) {
-    CostMfma<KX> c;
+    constexpr bool MMA = !std::is_same<Src, CostD>::value;
+    Src c;
     c.init(P, p, b);
     float* ring = sm.cost_ring(w);
     const int* done = sm.done() + w;
     int* ready = sm.ready() + w;
     int known = 0;
-    const int T = P.S / U + 1;  // tiles the compute wave reads
+    const int groups = P.S / U;  // groups of the compute wave
+    const int T = groups + 1;    // tiles it reads
     auto col = [&](int t) { return BWD ? P.M - TC * (t + 1) : TC * t; };
     c.issue(col(0));
     for (int t = 0; t < T; ++t) {
-        c.zero();
+        if constexpr (MMA) {
+            c.zero();
 #pragma unroll
-        for (int kk = 0; kk < CostMfma<KX>::NKK; ++kk) c.mma(kk);
-        const int need = BWD ? t - 2 : t - 4;
+            for (int kk = 0; kk < Src::NKK; ++kk) c.mma(kk);
+        }
+        const int need = BWD ? t - 3 : t - 4;
         if (need > 0 && !wait_at_least(done, need, known, P.err)) return;
-        c.finish(ring, col(t));
-        if (t + 1 < T) c.issue(col(t + 1));
+        GTile gt;
+        const bool flush = BWD && t >= 4;
+        if (flush) gt.read(P, ring, (t - 4) * U);
+        if constexpr (MMA) c.finish(ring, col(t));
+        else c.store(ring, col(t));
         if ((threadIdx.x & (WAVE - 1)) == 0) lds_publish(ready, t + 1);
+        if (t + 1 < T) c.issue(col(t + 1));
+        if (flush) gt.write(P, p, b);
+    }
+    if (BWD) {
+        for (int g = max(T - 4, 0); g < groups; ++g) {
+            if (!wait_at_least(done, g + 1, known, P.err)) return;
+            GTile gt;
+            gt.read(P, ring, g * U);
+            gt.write(P, p, b);
+        }
     }
 }
 
@@ -704,12 +770,17 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
 }
 
 // Waves of a workgroup: compute waves 0 .. W-1 (one band each) and the helper wave W; with
-// matrix-core costs (W <= 2), the producer waves W .. 2W-1 (of bands 0 .. W-1, on the SIMDs
-// the compute waves leave free when waves are placed round-robin) and the helper wave 2W.
-constexpr int kDPThreads = 5 * WAVE;
+// staged costs, the producer waves W .. 2W-1 (of bands 0 .. W-1) and the helper wave 2W.
+// Matrix-core producers run with W <= 2, so that under round-robin wave placement they take
+// the SIMDs the compute waves leave free; D producers (backward) share their compute wave's
+// SIMD (W <= 4).
+template <class Cost, bool BWD>
+constexpr int dp_threads() {
+    return Produced<Cost, BWD>::value && std::is_same<Cost, CostD>::value ? 9 * WAVE : 5 * WAVE;
+}
 
 template <class Cost, bool BAND, bool EXACT>
-__global__ void __launch_bounds__(kDPThreads) fwd_kernel(DPParams P) {
+__global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W), kTabBytesFwd};
     // wave-uniform values are moved to scalar registers so that the branches on band,
@@ -725,16 +796,16 @@ __global__ void __launch_bounds__(kDPThreads) fwd_kernel(DPParams P) {
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G, g = t - p * P.G;
-    if (w == (Produced<Cost>::value ? 2 * P.W : P.W)) {
+    if (w == (Produced<Cost, false>::value ? 2 * P.W : P.W)) {
         // helper wave: the previous workgroup's last row into ring 0
         if (g > 0) helper_wave(P, sm, P.gring + ((int64_t)p * P.G + (g - 1)) * P.RW + RPAD, 0);
         return;
     }
-    if constexpr (Produced<Cost>::value) {
+    if constexpr (Produced<Cost, false>::value) {
         const int wb = w >= P.W ? w - P.W : w;  // band of this compute or producer wave
         if (g * P.W + wb >= P.nb) return;
         if (w >= P.W) {
-            producer_wave<Cost::KXV, false>(P, sm, p, g * P.W + wb, wb);
+            producer_wave<Cost, false>(P, sm, p, g * P.W + wb, wb);
         } else {
             CostRing cost;
             cost.bind(sm, w, P.err);
@@ -792,9 +863,6 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const int* lin_flag = sm.prod() + (w + 1);
 
     const float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
-    // G tile stores: lane l covers column (l & 15) of rows 4k + (l >> 4) of the band
-    const int nrows = min(N - b * WAVE, WAVE);
-    float* Gband = P.G_out + ((int64_t)p * N + b * WAVE + (l >> 4)) * M + (l & 15);
 
     int known_in = 0, known_free = 0;
     float rE = 0.0f, rR = NINF, rD = 0.0f;  // right neighbour
@@ -843,28 +911,12 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // still live: at the end of group q0 the ring holds columns from the newest cost tile,
     // M - 48 - q0, up to M + 62 - q0, 111 < CR columns; writes of cells outside the table
     // land on slots of columns that are rewritten before use or already stored.
+    // (with costs from a producer wave, the producer stores the tiles)
     auto flush = [&](int q0) {
-        const int c0 = M + 47 - q0;
-        if (c0 >= M || c0 + TC <= 0) return;
-        const int col = c0 + (l & 15);
-        if ((unsigned)col >= (unsigned)M) return;
-        const float* src = cring + (l >> 4) * CS + (col & (CR - 1));
-        float v[16];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = src[4 * k * CS];
-        float* dst = Gband + c0;
-        if (nrows == WAVE) {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                *dst = v[k];
-                dst += 4 * M;
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                if (4 * k + (l >> 4) < nrows) *dst = v[k];
-                dst += 4 * M;
-            }
+        if constexpr (!std::is_same<Cost, CostRing>::value) {
+            GTile gt;
+            gt.read(P, cring, q0);
+            gt.write(P, p, b);
         }
     };
     // forward step of reverse step q, clamped into the band (padding steps are inactive)
@@ -970,7 +1022,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 }
 
 template <class Cost, bool BAND, bool EXACT>
-__global__ void __launch_bounds__(kDPThreads) bwd_kernel(DPParams P) {
+__global__ void __launch_bounds__((dp_threads<Cost, true>())) bwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W), kTabBytesBwd};
     // wave-uniform values are moved to scalar registers so that the branches on band,
@@ -984,16 +1036,16 @@ __global__ void __launch_bounds__(kDPThreads) bwd_kernel(DPParams P) {
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G;
     const int g = (P.G - 1) - (t - p * P.G);  // lowest ticket of a pair takes the bottom group
-    if (w == (Produced<Cost>::value ? 2 * P.W : P.W)) {
+    if (w == (Produced<Cost, true>::value ? 2 * P.W : P.W)) {
         // helper wave: the next workgroup's first row into ring W
         if (g + 1 < P.G) helper_wave(P, sm, P.gring4 + ((int64_t)p * P.G + (g + 1)) * P.RW + RPAD, P.W);
         return;
     }
-    if constexpr (Produced<Cost>::value) {
+    if constexpr (Produced<Cost, true>::value) {
         const int wb = w >= P.W ? w - P.W : w;
         if (g * P.W + wb >= P.nb) return;
         if (w >= P.W) {
-            producer_wave<Cost::KXV, true>(P, sm, p, g * P.W + wb, wb);
+            producer_wave<Cost, true>(P, sm, p, g * P.W + wb, wb);
         } else {
             CostRing cost;
             cost.bind(sm, w, P.err);
@@ -1038,11 +1090,11 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipSt
 template <class Cost, bool BWD, bool EXACT>
 hipError_t launch_cost(const DPParams& P, hipStream_t st) {
     if constexpr (BWD) {
-        if (P.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT>, P, true, Produced<Cost>::value, st);
-        return launch_dp(bwd_kernel<Cost, false, EXACT>, P, true, Produced<Cost>::value, st);
+        if (P.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT>, P, true, Produced<Cost, true>::value, st);
+        return launch_dp(bwd_kernel<Cost, false, EXACT>, P, true, Produced<Cost, true>::value, st);
     } else {
-        if (P.bw > 0.0) return launch_dp(fwd_kernel<Cost, true, EXACT>, P, false, Produced<Cost>::value, st);
-        return launch_dp(fwd_kernel<Cost, false, EXACT>, P, false, Produced<Cost>::value, st);
+        if (P.bw > 0.0) return launch_dp(fwd_kernel<Cost, true, EXACT>, P, false, Produced<Cost, false>::value, st);
+        return launch_dp(fwd_kernel<Cost, false, EXACT>, P, false, Produced<Cost, false>::value, st);
     }
 }
 
