@@ -163,11 +163,13 @@ int sdtw_debug_status(int op, const void* ws, size_t ws_bytes, int64_t B, int64_
     } else if (op != SDTW_OP_FWD && op != SDTW_OP_BWD) {
         return SDTW_OK;
     }
-    const DPScratch d = carve_dp(c, B, N, M);
-    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    // only the scratch header [ticket, error flag] is read; its place does not depend on
+    // the band geometry the launch chose
+    const int* hdr = c.take<int>(64);
+    if (!c.ok || !hdr) return SDTW_ERR_WORKSPACE;
     int flag = 0;
     if (hipDeviceSynchronize() != hipSuccess) return SDTW_ERR_LAUNCH;
-    if (hipMemcpy(&flag, d.err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+    if (hipMemcpy(&flag, hdr + 1, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
         return SDTW_ERR_LAUNCH;
     return flag ? SDTW_ERR_TIMEOUT : SDTW_OK;
 }
