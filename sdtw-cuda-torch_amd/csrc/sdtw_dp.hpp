@@ -874,10 +874,11 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     float4 dn_cur[U], hold[U];
     float r_cur[U], r_nxt[U], d_cur[U], d_nxt[U];
     // Band below: sequence numbers [q0, q0 + U) of its first row from the LDS ring, for
-    // lane 63.  Where no band lies below, or past sequence number M - 1, the values are
-    // unused (lane 63 then holds row N - 1, which takes the padding below directly, or is
-    // beyond the table or inactive); they are set to the padding (E 0, R -inf, D 0), which
-    // compiles to fewer live registers than leaving them stale.
+    // lane 63.  Where no band lies below, the values are the padding row below the table
+    // (E 0, R -inf, D 0): lane 63 then holds row N - 1 (or is beyond the table), and only the
+    // unmasked interior body takes them from here rather than from the padding directly.
+    // Past sequence number M - 1 lane 63 is inactive and the values are unused; they are
+    // set to the padding too, which compiles to fewer live registers than leaving them stale.
     auto fetch_lds = [&](int q0, float4* dst) -> bool {
 #pragma unroll
         for (int u = 0; u < U; ++u) dst[u] = make_float4(0.0f, NINF, 0.0f, 1.0f);
