@@ -167,6 +167,39 @@ int sdtw_fused_bwd_e_f32(const float *x, const float *y, const float *R, const f
                          float *E, int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
                          double bandwidth, void *ws, size_t ws_bytes, void *stream);
 
+/* ---- float64 path ------------------------------------------------------------------------
+ * The reference keeps the caller's dtype: float64 inputs give a float64 cost
+ * (distances.py:20-25) and float64 recursions (launcher.py:307-368, numba on float64 arrays),
+ * which torch.autograd.gradcheck needs (test_softdtw_small.py:29-37).  These entry points
+ * compute in double throughout.  R is the reference's dense (B, N+2, M+2) table
+ * (launcher.py:177, :310).  No workspace; one workgroup per pair sweeps its anti-diagonals,
+ * with no waits between workgroups.  B <= 65535. */
+
+/* Doubles of the float64 R table: B * (N+2) * (M+2). */
+int64_t sdtw_table_elems_f64(int64_t B, int64_t N, int64_t M);
+
+/* As sdtw_sqeuclid_fwd_f32, in double.  Replaces distances.py:6-28 for float64 inputs. */
+int sdtw_sqeuclid_fwd_f64(const double *x, const double *y, double *D, int64_t B, int64_t N,
+                          int64_t M, int64_t K, void *stream);
+
+/* As sdtw_sqeuclid_bwd_f32, in double (mask = 1: clamp_min mask from D; 0: none, the fused
+ * chain rule).  Replaces the autograd backward of distances.py:20-28 and, with mask = 0,
+ * autograd_xy.py:41-49, for float64 inputs. */
+int sdtw_sqeuclid_bwd_f64(const double *x, const double *y, const double *D, const double *G,
+                          double *gx, double *gy, int64_t B, int64_t N, int64_t M, int64_t K,
+                          int mask, void *stream);
+
+/* Forward over a float64 cost: R (B, N+2, M+2) and out[b] = R[b, N, M].  Replaces
+ * launcher.py:167-223 / :356-361 for float64 inputs (the arithmetic of launcher.py:307-324). */
+int sdtw_fwd_f64(const double *D, double *R, double *out, int64_t B, int64_t N, int64_t M,
+                 double gamma, double bandwidth, void *stream);
+
+/* Backward: G[b,i,j] = gout[b] * E[b,i,j] (gout NULL: G = E), R as sdtw_fwd_f64 wrote it
+ * (read only).  Replaces launcher.py:226-300 / :364-368 with autograd.py:46-47 for float64
+ * inputs (the arithmetic of launcher.py:327-353). */
+int sdtw_bwd_f64(const double *D, const double *R, const double *gout, double *G, int64_t B,
+                 int64_t N, int64_t M, double gamma, double bandwidth, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,272 @@
+// sdtw_f64.hip -- the float64 path: distance, recursions and distance backward in double.
+//
+// The reference keeps the caller's dtype end to end: for float64 inputs the cost is formed in
+// float64 (distances.py:20-25) and the recursions run on float64 arrays (launcher.py:307-368:
+// R is float64 and so are D, E and every difference), which is what torch.autograd.gradcheck
+// relies on (the reference's test_softdtw_small.py:29-37).  These kernels restate that
+// arithmetic in double, operation for operation:
+//   forward   R[i,j] = D[i-1,j-1] - gamma (log(sum_k exp(r_k - rmax)) + rmax),
+//             r_k = -R[nbr_k] / gamma, rmax the Python max (launcher.py:316-322);
+//   backward  E[i,j] = sum over the three later neighbours of E[nbr] exp((R[nbr] - R[i,j] -
+//             D[nbr]) / gamma), with R's +inf entries read as -inf and the padding of
+//             launcher.py:330-345;
+// with the Sakoe-Chiba test `0 < bandwidth < |i - j|` of launcher.py:315 and :345.
+//
+// Layout: R is the reference's own dense (B, N+2, M+2) table (row 0 / column 0 padding, row
+// N+1 / column M+1 read by the backward).  One workgroup owns a pair and sweeps it by
+// anti-diagonals: the cells of a diagonal are independent, so its threads compute them at
+// once and a workgroup barrier separates consecutive diagonals.  There are no waits between
+// workgroups.  The neighbours are read back from global memory (the workgroup's own writes,
+// made visible by the barrier), so any N and M fit.  This path favours a direct restatement
+// over speed: it exists so that float64 callers get float64 results.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/sdtw.h"
+
+namespace sdtw64 {
+
+constexpr int kSweepThreads = 1024;
+
+__device__ __forceinline__ bool out_of_band(double bw, int64_t i, int64_t j) {
+    const int64_t d = i > j ? i - j : j - i;
+    return 0.0 < bw && bw < (double)d;
+}
+
+// D[b,i,j] = max(0, (|x_i|^2 + |y_j|^2) - 2 x_i.y_j), the operation order of
+// distances.py:20-25 (norms and dot as sequential sums).  One thread per cell.
+__global__ void __launch_bounds__(256) dist_fwd_kernel(const double* __restrict__ x,
+                                                       const double* __restrict__ y,
+                                                       double* __restrict__ D, int N, int M,
+                                                       int K) {
+    const int j = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int i = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int64_t b = blockIdx.z;
+    if (i >= N || j >= M) return;
+    const double* xi = x + (b * N + i) * K;
+    const double* yj = y + (b * M + j) * K;
+    double x2 = 0.0, y2 = 0.0, dot = 0.0;
+    for (int k = 0; k < K; ++k) {
+        const double a = xi[k], c = yj[k];
+        x2 = fma(a, a, x2);
+        y2 = fma(c, c, y2);
+        dot = fma(a, c, dot);
+    }
+    const double pre = (x2 + y2) - 2.0 * dot;
+    D[(b * N + i) * M + j] = pre > 0.0 ? pre : (pre == pre ? 0.0 : pre);
+}
+
+// clamp_min's backward passes the gradient where the pre-clamp value is >= 0: every cell with
+// D > 0, and the cells with D == 0 whose pre-clamp value is exactly zero (recomputed with the
+// forward kernel's arithmetic, so with its bits).
+__device__ __forceinline__ double masked(double g, double d, const double* xi, const double* yj,
+                                         int K) {
+    if (d > 0.0) return g;
+    if (d != 0.0) return 0.0;  // NaN cost: torch's mask (NaN >= 0) is false
+    double x2 = 0.0, y2 = 0.0, dot = 0.0;
+    for (int k = 0; k < K; ++k) {
+        const double a = xi[k], c = yj[k];
+        x2 = fma(a, a, x2);
+        y2 = fma(c, c, y2);
+        dot = fma(a, c, dot);
+    }
+    return ((x2 + y2) - 2.0 * dot) >= 0.0 ? g : 0.0;
+}
+
+// gx[b,i,k] = 2 x[b,i,k] sum_j G'[b,i,j] - 2 sum_j G'[b,i,j] y[b,j,k]  (TRANS = false), and
+// gy[b,j,k] = 2 y[b,j,k] sum_i G'[b,i,j] - 2 sum_i G'[b,i,j] x[b,i,k]  (TRANS = true).
+// One thread per output element: 64 features of 4 output rows per block.
+template <bool TRANS>
+__global__ void __launch_bounds__(256) dist_bwd_kernel(const double* __restrict__ x,
+                                                       const double* __restrict__ y,
+                                                       const double* __restrict__ D,
+                                                       const double* __restrict__ G,
+                                                       double* __restrict__ out, int N, int M,
+                                                       int K, int mask) {
+    const int k = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int r = blockIdx.y * 4 + (threadIdx.x >> 6);  // output row: i (gx) or j (gy)
+    const int64_t b = blockIdx.z;
+    const int R = TRANS ? M : N, T = TRANS ? N : M;     // output rows, reduction length
+    if (r >= R) return;
+    const double* self = (TRANS ? y + (b * M + r) * K : x + (b * N + r) * K);
+    const double* other = TRANS ? x + b * N * K : y + b * M * K;
+    const double* Gb = G + b * N * M;
+    const double* Db = mask ? D + b * N * M : nullptr;  // D is not passed without the mask
+    const bool kin = k < K;
+    double s = 0.0, acc = 0.0;
+    for (int t = 0; t < T; ++t) {
+        const int64_t cell = TRANS ? (int64_t)t * M + r : (int64_t)r * M + t;
+        const double* xi = TRANS ? other + (int64_t)t * K : self;
+        const double* yj = TRANS ? self : other + (int64_t)t * K;
+        const double g = Db ? masked(Gb[cell], Db[cell], xi, yj, K) : Gb[cell];
+        s += g;
+        if (kin) acc = fma(g, other[(int64_t)t * K + k], acc);
+    }
+    if (kin) out[(b * R + r) * K + k] = 2.0 * s * self[k] - 2.0 * acc;
+}
+
+// Forward recursion of pair blockIdx.x (launcher.py:307-324), R (N+2, M+2) dense.
+__global__ void __launch_bounds__(kSweepThreads) dp_fwd_kernel(const double* __restrict__ Dall,
+                                                               double* __restrict__ Rall,
+                                                               double* __restrict__ out, int N,
+                                                               int M, double gamma, double bw) {
+    const int64_t b = blockIdx.x;
+    const int64_t W = M + 2;
+    double* R = Rall + b * (N + 2) * W;
+    const double* D = Dall + b * N * M;
+    const double INF = __builtin_inf();
+    for (int64_t e = threadIdx.x; e < (N + 2) * W; e += blockDim.x) R[e] = e == 0 ? 0.0 : INF;
+    __syncthreads();
+    for (int d = 2; d <= N + M; ++d) {
+        const int ilo = d - M > 1 ? d - M : 1;
+        const int ihi = d - 1 < N ? d - 1 : N;
+        for (int i = ilo + threadIdx.x; i <= ihi; i += blockDim.x) {
+            const int j = d - i;
+            if (out_of_band(bw, i, j)) continue;
+            const double r0 = -R[(i - 1) * W + (j - 1)] / gamma;
+            const double r1 = -R[(i - 1) * W + j] / gamma;
+            const double r2 = -R[i * W + (j - 1)] / gamma;
+            double rmax = (r1 > r0) ? r1 : r0;
+            rmax = (r2 > rmax) ? r2 : rmax;
+            const double rsum = exp(r0 - rmax) + exp(r1 - rmax) + exp(r2 - rmax);
+            const double softmin = -gamma * (log(rsum) + rmax);
+            R[i * W + j] = D[(int64_t)(i - 1) * M + (j - 1)] + softmin;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[b] = R[N * W + M];
+}
+
+// Backward of pair blockIdx.x (launcher.py:327-353) into G (N, M): E is formed in G (its
+// padding row and column are read as launcher.py:330-338 sets them: E 0 but E[N+1,M+1] = 1;
+// R -inf but R[N+1,M+1] = R[N,M]; D 0), then scaled by gout[b].  R itself is not modified:
+// its +inf entries are read as -inf, as the reference's in-place edit (launcher.py:343-344)
+// leaves them for every later read.
+__global__ void __launch_bounds__(kSweepThreads) dp_bwd_kernel(const double* __restrict__ Dall,
+                                                               const double* __restrict__ Rall,
+                                                               const double* __restrict__ gout,
+                                                               double* __restrict__ Gall, int N,
+                                                               int M, double gamma, double bw) {
+    const int64_t b = blockIdx.x;
+    const int64_t W = M + 2;
+    const double* R = Rall + b * (N + 2) * W;
+    const double* D = Dall + b * N * M;
+    double* E = Gall + b * N * M;
+    const double NINF = -__builtin_inf();
+    const double corner = R[N * W + M];  // R[N+1, M+1], set before the sweep's edits
+    auto Rat = [&](int i, int j) -> double {
+        if (i > N || j > M) return (i > N && j > M) ? corner : NINF;
+        const double v = R[i * W + j];
+        return isinf(v) ? NINF : v;
+    };
+    auto Eat = [&](int i, int j) -> double {
+        if (i > N || j > M) return (i > N && j > M) ? 1.0 : 0.0;
+        return E[(int64_t)(i - 1) * M + (j - 1)];
+    };
+    auto Dat = [&](int i, int j) -> double {
+        if (i > N || j > M) return 0.0;
+        return D[(int64_t)(i - 1) * M + (j - 1)];
+    };
+    for (int64_t e = threadIdx.x; e < (int64_t)N * M; e += blockDim.x) E[e] = 0.0;
+    __syncthreads();
+    for (int d = N + M; d >= 2; --d) {
+        const int ilo = d - M > 1 ? d - M : 1;
+        const int ihi = d - 1 < N ? d - 1 : N;
+        for (int i = ilo + threadIdx.x; i <= ihi; i += blockDim.x) {
+            const int j = d - i;
+            if (out_of_band(bw, i, j)) continue;
+            const double rij = Rat(i, j);
+            const double da = (Rat(i + 1, j) - rij) - Dat(i + 1, j);
+            const double db = (Rat(i, j + 1) - rij) - Dat(i, j + 1);
+            const double dc = (Rat(i + 1, j + 1) - rij) - Dat(i + 1, j + 1);
+            const double a = exp(da / gamma);
+            const double bb = exp(db / gamma);
+            const double c = exp(dc / gamma);
+            double acc = Eat(i + 1, j) * a;
+            acc = acc + Eat(i, j + 1) * bb;
+            acc = acc + Eat(i + 1, j + 1) * c;
+            E[(int64_t)(i - 1) * M + (j - 1)] = acc;
+        }
+        __syncthreads();
+    }
+    if (gout) {
+        const double g = gout[b];
+        for (int64_t e = threadIdx.x; e < (int64_t)N * M; e += blockDim.x) E[e] = g * E[e];
+    }
+}
+
+bool shape_ok(int64_t B, int64_t N, int64_t M, int64_t K, bool need_k) {
+    if (B < 0 || N <= 0 || M <= 0 || B > 65535) return false;
+    if (need_k && (K <= 0 || K > INT32_MAX)) return false;
+    // int row / diagonal indices; the grids put rows / 4 on grid.y
+    if (N > INT32_MAX / 2 - 2 || M > INT32_MAX / 2 - 2) return false;
+    if ((N + 3) / 4 > 65535 || (M + 3) / 4 > 65535) return false;
+    return true;
+}
+
+int status_of(hipError_t e) { return e == hipSuccess ? SDTW_OK : SDTW_ERR_LAUNCH; }
+
+}  // namespace sdtw64
+
+using namespace sdtw64;
+
+extern "C" {
+
+int64_t sdtw_table_elems_f64(int64_t B, int64_t N, int64_t M) {
+    if (B < 0 || N <= 0 || M <= 0) return 0;
+    return B * (N + 2) * (M + 2);
+}
+
+int sdtw_sqeuclid_fwd_f64(const double* x, const double* y, double* D, int64_t B, int64_t N,
+                          int64_t M, int64_t K, void* stream) {
+    if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!x || !y || !D) return SDTW_ERR_INVALID_VALUE;
+    hipLaunchKernelGGL(dist_fwd_kernel, dim3((unsigned)((M + 63) / 64), (unsigned)((N + 3) / 4),
+                                             (unsigned)B),
+                       dim3(256), 0, (hipStream_t)stream, x, y, D, (int)N, (int)M, (int)K);
+    return status_of(hipGetLastError());
+}
+
+int sdtw_sqeuclid_bwd_f64(const double* x, const double* y, const double* D, const double* G,
+                          double* gx, double* gy, int64_t B, int64_t N, int64_t M, int64_t K,
+                          int mask, void* stream) {
+    if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!x || !y || !G || !gx || !gy || (mask && !D)) return SDTW_ERR_INVALID_VALUE;
+    if ((K + 63) / 64 > INT32_MAX) return SDTW_ERR_UNSUPPORTED;
+    const hipStream_t st = (hipStream_t)stream;
+    const unsigned kb = (unsigned)((K + 63) / 64);
+    hipLaunchKernelGGL(dist_bwd_kernel<false>, dim3(kb, (unsigned)((N + 3) / 4), (unsigned)B),
+                       dim3(256), 0, st, x, y, D, G, gx, (int)N, (int)M, (int)K, mask);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return SDTW_ERR_LAUNCH;
+    hipLaunchKernelGGL(dist_bwd_kernel<true>, dim3(kb, (unsigned)((M + 3) / 4), (unsigned)B),
+                       dim3(256), 0, st, x, y, D, G, gy, (int)N, (int)M, (int)K, mask);
+    return status_of(hipGetLastError());
+}
+
+int sdtw_fwd_f64(const double* D, double* R, double* out, int64_t B, int64_t N, int64_t M,
+                 double gamma, double bandwidth, void* stream) {
+    if (!shape_ok(B, N, M, 1, false)) return SDTW_ERR_INVALID_VALUE;
+    if (!(gamma > 0.0) || !isfinite(gamma)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!D || !R || !out) return SDTW_ERR_INVALID_VALUE;
+    hipLaunchKernelGGL(dp_fwd_kernel, dim3((unsigned)B), dim3(kSweepThreads), 0,
+                       (hipStream_t)stream, D, R, out, (int)N, (int)M, gamma, bandwidth);
+    return status_of(hipGetLastError());
+}
+
+int sdtw_bwd_f64(const double* D, const double* R, const double* gout, double* G, int64_t B,
+                 int64_t N, int64_t M, double gamma, double bandwidth, void* stream) {
+    if (!shape_ok(B, N, M, 1, false)) return SDTW_ERR_INVALID_VALUE;
+    if (!(gamma > 0.0) || !isfinite(gamma)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!D || !R || !G) return SDTW_ERR_INVALID_VALUE;
+    hipLaunchKernelGGL(dp_bwd_kernel, dim3((unsigned)B), dim3(kSweepThreads), 0,
+                       (hipStream_t)stream, D, R, gout, G, (int)N, (int)M, gamma, bandwidth);
+    return status_of(hipGetLastError());
+}
+
+}  // extern "C"

@@ -56,6 +56,15 @@ _SIGS = {
     "sdtw_fused_bwd_e_f32": ([ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4
                              + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                              ctypes.c_int),
+    "sdtw_table_elems_f64": ([ctypes.c_int64] * 3, ctypes.c_int64),
+    "sdtw_sqeuclid_fwd_f64": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4 + [ctypes.c_void_p],
+                              ctypes.c_int),
+    "sdtw_sqeuclid_bwd_f64": ([ctypes.c_void_p] * 6 + [ctypes.c_int64] * 4
+                              + [ctypes.c_int, ctypes.c_void_p], ctypes.c_int),
+    "sdtw_fwd_f64": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3 + [ctypes.c_double] * 2
+                     + [ctypes.c_void_p], ctypes.c_int),
+    "sdtw_bwd_f64": ([ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3 + [ctypes.c_double] * 2
+                     + [ctypes.c_void_p], ctypes.c_int),
 }
 
 
@@ -118,11 +127,11 @@ def _check(rc: int, what: str):
         raise RuntimeError(f"softdtw_cuda: {what} failed: {strerror(rc)} (status {rc})")
 
 
-def require_gpu(t: torch.Tensor, what: str):
+def require_gpu(t: torch.Tensor, what: str, dtype=torch.float32):
     if not t.is_cuda:
         raise RuntimeError(f"softdtw_cuda: {what} expects a ROCm/CUDA tensor, got {t.device}")
-    if t.dtype != torch.float32 or not t.is_contiguous():
-        raise RuntimeError(f"softdtw_cuda: {what} expects contiguous float32, got {t.dtype}")
+    if t.dtype != dtype or not t.is_contiguous():
+        raise RuntimeError(f"softdtw_cuda: {what} expects contiguous {dtype}, got {t.dtype}")
 
 
 def table_elems(B, N, M) -> int:
@@ -333,3 +342,77 @@ def fused_bwd_e(x, y, R, gamma: float, bandwidth: float, gout=None):
     _check(rc, "fused backward (E)")
     _debug_check(OP_FUSED_BWD, ws, nws, B, N, M, K, "fused backward (E)")
     return E
+
+
+# ---- float64 path (sdtw_*_f64): double throughout, R the dense (B, N+2, M+2) table -------
+F64 = torch.float64
+
+
+def sqeuclid_fwd64(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    require_gpu(x, "sqeuclid x", F64)
+    require_gpu(y, "sqeuclid y", F64)
+    _check_shapes(x=x, y=y)
+    B, N, K = x.shape
+    M = y.shape[1]
+    D = torch.empty((B, N, M), dtype=F64, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = load().sdtw_sqeuclid_fwd_f64(_ptr(x), _ptr(y), _ptr(D), B, N, M, K, _stream(x.device))
+    _check(rc, "sqeuclid forward (float64)")
+    return D
+
+
+def sqeuclid_bwd64(x, y, D, G, mask: bool = True):
+    for t, n in ((x, "x"), (y, "y"), (G, "G")):
+        require_gpu(t, f"sqeuclid backward {n}", F64)
+    if mask:
+        require_gpu(D, "sqeuclid backward D", F64)
+    _check_shapes(x=x, y=y, D=G)
+    if mask:
+        _check_shapes(x=x, y=y, D=D)
+    B, N, K = x.shape
+    M = y.shape[1]
+    gx = torch.empty_like(x)
+    gy = torch.empty_like(y)
+    with torch.cuda.device(x.device):
+        rc = load().sdtw_sqeuclid_bwd_f64(_ptr(x), _ptr(y), _ptr(D if mask else None), _ptr(G),
+                                          _ptr(gx), _ptr(gy), B, N, M, K, 1 if mask else 0,
+                                          _stream(x.device))
+    _check(rc, "sqeuclid backward (float64)")
+    return gx, gy
+
+
+def _check_table64(R, B, N, M):
+    if tuple(R.shape) != (B, N + 2, M + 2):
+        raise ValueError(f"softdtw_cuda: float64 R must be (B,N+2,M+2)={(B, N + 2, M + 2)}, "
+                         f"got {tuple(R.shape)}")
+
+
+def dtw_fwd64(D: torch.Tensor, gamma: float, bandwidth: float):
+    """(out (B,), R (B, N+2, M+2)), both float64."""
+    require_gpu(D, "softdtw forward D", F64)
+    _check_shapes(D=D)
+    B, N, M = D.shape
+    R = torch.empty((B, N + 2, M + 2), dtype=F64, device=D.device)
+    out = torch.empty((B,), dtype=F64, device=D.device)
+    with torch.cuda.device(D.device):
+        rc = load().sdtw_fwd_f64(_ptr(D), _ptr(R), _ptr(out), B, N, M, float(gamma),
+                                 float(bandwidth), _stream(D.device))
+    _check(rc, "softdtw forward (float64)")
+    return out, R
+
+
+def dtw_bwd64(D, R, gamma: float, bandwidth: float, gout=None):
+    """G = gout * E (B, N, M) float64; gout None gives E."""
+    require_gpu(D, "softdtw backward D", F64)
+    require_gpu(R, "softdtw backward R", F64)
+    if gout is not None:
+        require_gpu(gout, "softdtw backward grad_output", F64)
+    _check_shapes(D=D, gout=gout)
+    B, N, M = D.shape
+    _check_table64(R, B, N, M)
+    G = torch.empty((B, N, M), dtype=F64, device=D.device)
+    with torch.cuda.device(D.device):
+        rc = load().sdtw_bwd_f64(_ptr(D), _ptr(R), _ptr(gout), _ptr(G), B, N, M, float(gamma),
+                                 float(bandwidth), _stream(D.device))
+    _check(rc, "softdtw backward (float64)")
+    return G

@@ -4,7 +4,7 @@ import torch
 from torch.autograd import Function
 
 from . import _engine
-from ._device import compute_device, to_engine
+from ._device import compute_device, engine_dtype, to_engine
 from .utils.checks import check_D
 
 
@@ -20,7 +20,9 @@ class SoftDTWAutograd(Function):
     """Soft-DTW over a materialised cost D (B,N,M) -> (B,).
 
     Forward: sdtw_fwd_f32 (fp64 recursion, R stored fp32 once).  Backward:
-    sdtw_bwd_f32 returns grad_D = g * E directly (reference autograd.py:11-48)."""
+    sdtw_bwd_f32 returns grad_D = g * E directly (reference autograd.py:11-48).  A float64 D
+    takes sdtw_fwd_f64 / sdtw_bwd_f64 (double throughout, as the reference's CPU path
+    computes float64 inputs)."""
 
     @staticmethod
     def forward(ctx, D: torch.Tensor, gamma: float, bandwidth: float | None):
@@ -30,8 +32,10 @@ class SoftDTWAutograd(Function):
             raise ValueError(f"gamma must be > 0, got {gamma_f}")
         bandwidth_f = _normalize_bandwidth(bandwidth)
         dev = compute_device(D)
-        Dg = to_engine(D.detach(), dev)
-        out, R = _engine.dtw_fwd(Dg, gamma_f, bandwidth_f)
+        dt = engine_dtype(D)
+        Dg = to_engine(D.detach(), dev, dt)
+        fwd = _engine.dtw_fwd64 if dt == torch.float64 else _engine.dtw_fwd
+        out, R = fwd(Dg, gamma_f, bandwidth_f)
         ctx.save_for_backward(Dg, R)
         ctx.gamma = gamma_f
         ctx.bandwidth = bandwidth_f
@@ -41,7 +45,8 @@ class SoftDTWAutograd(Function):
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor):
         Dg, R = ctx.saved_tensors
-        g = grad_output.reshape(-1).to(device=Dg.device, dtype=torch.float32).contiguous()
-        G = _engine.dtw_bwd(Dg, R, ctx.gamma, ctx.bandwidth, gout=g)
+        g = grad_output.reshape(-1).to(device=Dg.device, dtype=Dg.dtype).contiguous()
+        bwd = _engine.dtw_bwd64 if Dg.dtype == torch.float64 else _engine.dtw_bwd
+        G = bwd(Dg, R, ctx.gamma, ctx.bandwidth, gout=g)
         dev, dt = ctx.orig
         return G.to(device=dev, dtype=dt), None, None

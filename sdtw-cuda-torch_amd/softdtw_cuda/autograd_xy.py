@@ -4,7 +4,7 @@ import torch
 from torch.autograd import Function
 
 from . import _engine
-from ._device import to_engine
+from ._device import engine_dtype, to_engine
 from .autograd import _normalize_bandwidth
 
 
@@ -13,7 +13,10 @@ class SoftDTWXYAutograd(Function):
     (B,N,M) cost tensor is formed (reference autograd_xy.py:12-51).
 
     Forward: sdtw_fused_fwd_f32.  Backward: sdtw_fused_bwd_f32 returns
-    grad_X = 2 (X * sum_j gE - gE Y), grad_Y = 2 (Y * sum_i gE - gE^T X), gE = g * E."""
+    grad_X = 2 (X * sum_j gE - gE Y), grad_Y = 2 (Y * sum_i gE - gE^T X), gE = g * E.
+    float64 X, Y take the float64 kernels: the cost is formed (sdtw_sqeuclid_fwd_f64), the
+    recursions run on it (sdtw_fwd_f64 / sdtw_bwd_f64), and the same chain rule without a
+    clamp mask gives the gradients (sdtw_sqeuclid_bwd_f64, mask 0)."""
 
     @staticmethod
     def forward(ctx, X: torch.Tensor, Y: torch.Tensor, gamma: float, bandwidth: float | None):
@@ -26,13 +29,19 @@ class SoftDTWXYAutograd(Function):
         gamma_f = float(gamma)
         if not gamma_f > 0:
             raise ValueError(f"gamma must be > 0, got {gamma_f}")
-        Xg = to_engine(X.detach(), X.device)
-        Yg = to_engine(Y.detach(), X.device)
+        dt = engine_dtype(X, Y)
+        Xg = to_engine(X.detach(), X.device, dt)
+        Yg = to_engine(Y.detach(), X.device, dt)
         # forward takes the band as given (-1 for None), the backward normalised
         # (reference autograd_xy.py:16, :22-27); both disable it for values <= 0.
         bw_fwd = -1.0 if bandwidth is None else float(bandwidth)
-        out, R = _engine.fused_fwd(Xg, Yg, gamma_f, bw_fwd)
-        ctx.save_for_backward(Xg, Yg, R)
+        if dt == torch.float64:
+            D = _engine.sqeuclid_fwd64(Xg, Yg)
+            out, R = _engine.dtw_fwd64(D, gamma_f, bw_fwd)
+            ctx.save_for_backward(Xg, Yg, R, D)
+        else:
+            out, R = _engine.fused_fwd(Xg, Yg, gamma_f, bw_fwd)
+            ctx.save_for_backward(Xg, Yg, R)
         ctx.gamma = gamma_f
         ctx.bandwidth = _normalize_bandwidth(bandwidth)
         ctx.dtypes = (X.dtype, Y.dtype)
@@ -40,8 +49,13 @@ class SoftDTWXYAutograd(Function):
 
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor):
-        Xg, Yg, R = ctx.saved_tensors
-        g = grad_output.reshape(-1).to(device=Xg.device, dtype=torch.float32).contiguous()
-        gx, gy = _engine.fused_bwd(Xg, Yg, R, ctx.gamma, ctx.bandwidth, gout=g)
+        Xg, Yg, R = ctx.saved_tensors[:3]
+        g = grad_output.reshape(-1).to(device=Xg.device, dtype=Xg.dtype).contiguous()
+        if Xg.dtype == torch.float64:
+            D = ctx.saved_tensors[3]
+            G = _engine.dtw_bwd64(D, R, ctx.gamma, ctx.bandwidth, gout=g)
+            gx, gy = _engine.sqeuclid_bwd64(Xg, Yg, None, G, mask=False)
+        else:
+            gx, gy = _engine.fused_bwd(Xg, Yg, R, ctx.gamma, ctx.bandwidth, gout=g)
         dx, dy = ctx.dtypes
         return gx.to(dtype=dx), gy.to(dtype=dy), None, None

@@ -4,7 +4,7 @@ import torch
 from torch.autograd import Function
 
 from . import _engine
-from ._device import compute_device, to_engine
+from ._device import compute_device, engine_dtype, to_engine
 
 
 class _SqEuclideanHIP(Function):
@@ -26,6 +26,24 @@ class _SqEuclideanHIP(Function):
                 gy if ctx.needs_input_grad[1] else None)
 
 
+class _SqEuclideanHIP64(Function):
+    """The same distance and chain rule in double (sdtw_sqeuclid_fwd_f64 / _bwd_f64) for
+    float64 inputs, which the reference computes in float64 (distances.py:20-25)."""
+
+    @staticmethod
+    def forward(ctx, x, y):
+        D = _engine.sqeuclid_fwd64(x, y)
+        ctx.save_for_backward(x, y, D)
+        return D
+
+    @staticmethod
+    def backward(ctx, G):
+        x, y, D = ctx.saved_tensors
+        gx, gy = _engine.sqeuclid_bwd64(x, y, D, G.contiguous().to(torch.float64), mask=True)
+        return (gx if ctx.needs_input_grad[0] else None,
+                gy if ctx.needs_input_grad[1] else None)
+
+
 def sqeuclidean(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
     """
     Squared Euclidean distance D[b,i,j] = ||x[b,i]-y[b,j]||^2, computed on the GPU as
@@ -38,8 +56,10 @@ def sqeuclidean(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
     if x.shape[0] != y.shape[0] or x.shape[2] != y.shape[2]:
         raise ValueError(f"Batch/features mismatch: {tuple(x.shape)} vs {tuple(y.shape)}")
     dev = compute_device(x)
-    D = _SqEuclideanHIP.apply(to_engine(x, dev), to_engine(y, dev))
-    return D.to(device=x.device, dtype=x.dtype)
+    dt = engine_dtype(x, y)
+    fn = _SqEuclideanHIP64 if dt == torch.float64 else _SqEuclideanHIP
+    D = fn.apply(to_engine(x, dev, dt), to_engine(y, dev, dt))
+    return D.to(device=x.device, dtype=torch.promote_types(x.dtype, y.dtype))
 
 
 def pairwise_distance(x: torch.Tensor, y: torch.Tensor, *, dist: str) -> torch.Tensor:
