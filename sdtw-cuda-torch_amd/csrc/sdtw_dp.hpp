@@ -871,7 +871,11 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     float gD = 0.0f;
     float pE = 0.0f, pR = NINF, pD = 0.0f;  // published one step ago
 
-    float4 dn_cur[U], hold[U];
+    float4 dn_cur[U];
+    // lane 0's (E, R, D) of each step, shifted one lane up per step: after the group's last
+    // step lane k (< U) holds the entry of step U - 1 - k, so the handover is one wide write
+    // (or one pair of global stores) instead of U single-lane ones
+    float capE = 0.0f, capR = 0.0f, capD = 0.0f;
     float r_cur[U], r_nxt[U], d_cur[U], d_nxt[U];
     // Band below: sequence numbers [q0, q0 + U) of its first row from the LDS ring, for
     // lane 63.  Where no band lies below, the values are the padding row below the table
@@ -891,18 +895,17 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         return true;
     };
     // hand the band's first row to the band above: lane 0 produced sequence numbers
-    // q - 63 (= M - 1 - j) during the group at q0 (LDS writes unconditional, as in the
-    // forward)
+    // q - 63 (= M - 1 - j) during the group at q0, now held by lanes 0 .. U - 1 (LDS writes
+    // unconditional, as in the forward; the count is published after them)
     auto handover = [&](int q0) {
-        if (l != 0) return;
+        if (l >= U) return;
         const int c0 = q0 - (WAVE - 1);
+        const float4 v = make_float4(capE, capR, capD, 1.0f);
         if (out_lds) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) lout[hslot(c0) + u] = hold[u];
-            lds_publish(sm.prod() + w, min(max(q0 + U - (WAVE - 1), 0), M));
+            lout[hslot(c0) + (U - 1 - l)] = v;
+            if (l == 0) lds_publish(sm.prod() + w, min(max(q0 + U - (WAVE - 1), 0), M));
         } else {
-#pragma unroll
-            for (int u = 0; u < U; ++u) glb_put4(gout + c0 + u, hold[u]);
+            glb_put4(gout + c0 + (U - 1 - l), v);
         }
     };
     // Each step writes g*E of the lane's cell into the cost-ring slot whose cost it has just
@@ -996,7 +999,9 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             pE = mE;
             pR = mR;
             pD = mD;
-            hold[u] = make_float4(mE, mR, mD, 1.0f);
+            capE = __int_as_float(dpp_shr1(__float_as_int(mE), __float_as_int(capE)));
+            capR = __int_as_float(dpp_shr1(__float_as_int(mR), __float_as_int(capR)));
+            capD = __int_as_float(dpp_shr1(__float_as_int(mD), __float_as_int(capD)));
             // next group's R and costs, and the tile work, between the steps (fstep clamps
             // reads past the band's first step)
             r_nxt[u] = Rt[(int64_t)fstep(n0 + u) * WAVE];
