@@ -60,6 +60,12 @@ SDTW_DEV double shr1(double old, double v) {
     const int hi = dpp_shr1(__double2hiint(old), __double2hiint(v));
     return __hiloint2double(hi, lo);
 }
+// lane l receives lane l+1's v; lane 63 receives `old`
+SDTW_DEV double shl1(double old, double v) {
+    const int lo = dpp_shl1(__double2loint(old), __double2loint(v));
+    const int hi = dpp_shl1(__double2hiint(old), __double2hiint(v));
+    return __hiloint2double(hi, lo);
+}
 
 // LDS counters: relaxed accesses.  All LDS operations of a CU are performed as wave-wide
 // operations in one global order, a wave's in issue order, so a counter stored after ring
@@ -630,7 +636,11 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     double diag = (b == 0 && l == 0) ? 0.0 : INF;
     double prev = INF;   // this lane's value one step ago (sent to lane l+1 by DPP)
 
-    double up_cur[U], hold[U];
+    double up_cur[U];
+    // lane 63's value of each step, shifted one lane down per step: after the group's last
+    // step lane 63 - U + 1 + u holds the value of step u, so the handover is one wide write
+    // (or one global store) instead of U single-lane ones
+    double cap = INF;
     float d_cur[U], d_nxt[U];
 
     // Band above: columns [c0, c0 + U) of its last row from the LDS ring, for lane 0.  The
@@ -657,16 +667,15 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // s0 + u - 63 at step s0 + u) to the band below.  The LDS writes are unconditional:
     // slots of columns < 0 or >= M are never read before being rewritten or at all.
     auto handover = [&](int s0) {
-        if (l != WAVE - 1) return;
+        if (l < WAVE - U) return;
         const int c0 = s0 - (WAVE - 1);
+        const int u = l - (WAVE - U);  // step of the value this lane holds
         if (out_lds) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) lout[hslot(c0) + u] = hold[u];
-            lds_publish(sm.prod() + (w + 1), min(max(s0 + U - (WAVE - 1), 0), M));
+            lout[hslot(c0) + u] = cap;
+            if (l == WAVE - 1) lds_publish(sm.prod() + (w + 1), min(max(s0 + U - (WAVE - 1), 0), M));
         } else {
             // columns in [-63, M + 15]: inside the row's padding, no test needed
-#pragma unroll
-            for (int u = 0; u < U; ++u) glb_put(gout + c0 + u, hold[u]);
+            glb_put(gout + c0 + u, cap);
         }
     };
 
@@ -715,7 +724,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             left = r;
             diag = up;
             prev = r;
-            hold[u] = r;
+            cap = shl1(r, cap);
             Rg[u * WAVE] = (float)r;
             // next group's costs, and the tile work, between the steps
             d_nxt[u] = crow[(s0 + TC + u - l) & (CR - 1)];
