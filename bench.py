@@ -7,7 +7,7 @@ resident inputs, as in the reference's bench/bench_memory.py:51-58.  Both modes 
 unfused (materialised (B,N,M) cost) and fused (cost recomputed per cell).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--mode both|unfused|fused]
-                    [--no-cpu-baseline] [--kernel NAME --launches L]
+                    [--no-cpu-baseline] [--kernel NAME --launches L] [--grid]
 
 `value` is unfused DP cells/s = B*N*M / (fwd+bwd seconds); the fused figures ride along in
 the same line.  `roofline` covers the dominant kernel (largest share of a step), timed with
@@ -32,6 +32,22 @@ HBM_PEAK_GBS = 8000.0
 # reference CSV artefact, bench/softdtw_memory_benchmark.csv:13 (unfused 20.102 ms)
 REF_UNFUSED_MS = 20.102
 REF_FUSED_MS = 141.358
+
+
+# The reference's benchmark grid and its own timings (bench/bench_memory.py:163-167 for the
+# configurations, bench/softdtw_memory_benchmark.csv:2-17 for the figures: columns
+# ours_unfused_ms and ours_fused_ms, its engine on an unstated NVIDIA GPU): B, N = M, D,
+# unfused ms, fused ms.
+REF_GRID = [
+    (16, 128, 1, 2.1553, 36.7759), (16, 128, 64, 2.1559, 35.9518),
+    (16, 512, 1, 21.1427, 139.8459), (16, 512, 64, 19.3399, 141.8058),
+    (16, 1024, 1, 71.2458, 281.7823), (16, 1024, 64, 71.7209, 278.0873),
+    (16, 2048, 1, 489.8424, 557.3357), (16, 2048, 64, 484.7632, 592.2209),
+    (32, 128, 1, 1.8979, 35.7862), (32, 128, 64, 1.9554, 35.9961),
+    (32, 512, 1, 19.6090, 140.4723), (32, 512, 64, 20.1023, 141.3577),
+    (32, 1024, 1, 73.6546, 281.0321), (32, 1024, 64, 75.2204, 288.9885),
+    (32, 2048, 1, 489.4542, 567.0535), (32, 2048, 64, 491.6920, 1838.2080),
+]
 
 
 def log(msg):
@@ -181,6 +197,45 @@ def cpu_baseline(x, y, gamma, budget_s=15.0):
     }
 
 
+def run_grid(numerics):
+    """The reference's grid, timed as its bench_memory.py:24-58 does (fresh leaf clones,
+    fwd + sum + bwd per step; one warm-up, then the mean of 5 between events)."""
+    import torch
+
+    from softdtw_cuda import SoftDTW
+
+    rows = []
+    for B, N, K, ref_u, ref_f in REF_GRID:
+        x, y = make_inputs(B, N, N, K, seed=0)
+        X, Y = x.cuda(), y.cuda()
+        row = {"B": B, "N": N, "M": N, "D": K}
+        for mode, ref in (("unfused", ref_u), ("fused", ref_f)):
+            sdtw = SoftDTW(gamma=1.0, fused=(mode == "fused"))
+
+            def step():
+                xs = X.detach().clone().requires_grad_(True)
+                ys = Y.detach().clone().requires_grad_(True)
+                sdtw(xs, ys).sum().backward()
+
+            torch.cuda.empty_cache()
+            ms, peak = time_steps(step, 5, 1)
+            row[mode] = {"ms": round(ms, 4), "peak_mib": round(peak, 2), "reference_ms": ref,
+                         "speedup": round(ref / ms, 2)}
+            log(f"[grid] B={B} N=M={N} D={K} {mode}: {ms:.3f} ms (reference {ref} ms, "
+                f"{ref / ms:.1f}x), peak {peak:.1f} MiB")
+        rows.append(row)
+        del X, Y
+    line = {
+        "metric": "fwd+bwd ms per step over the reference's benchmark grid",
+        "unit": "ms", "higher_is_better": False, "n_gpus": 1, "numerics": numerics,
+        "dtype": "f32 (fp64 DP state)", "data": "synthetic (randn seed 0, y drawn after x)",
+        "reference_source": "bench/softdtw_memory_benchmark.csv:2-17 (unstated NVIDIA GPU)",
+        "grid": rows,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -194,6 +249,10 @@ def main(argv=None):
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--shape", default=None,
                     help="B,N,M,D for --kernel runs (default: the headline 32,512,512,64)")
+    ap.add_argument("--grid", action="store_true",
+                    help="time the reference's benchmark grid (16 configurations, unfused and "
+                         "fused, its protocol: one warm-up step, then the mean of 5) and print "
+                         "one JSON line with the reference's figures beside ours")
     ap.add_argument("--numerics", choices=["mixed", "exact", "fast"], default="mixed",
                     help="cell arithmetic of the recursions (mixed, the default: forward "
                          "bit-identical to the reference CPU path, backward weights in fp32; "
@@ -213,6 +272,9 @@ def main(argv=None):
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         return 1
     set_numerics(args.numerics)
+
+    if args.grid:
+        return run_grid(args.numerics)
 
     B, N, M, K, gamma = 32, 512, 512, 64, 1.0
     cells = B * N * M
