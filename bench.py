@@ -7,7 +7,7 @@ resident inputs, as in the reference's bench/bench_memory.py:51-58.  Both modes 
 unfused (materialised (B,N,M) cost) and fused (cost recomputed per cell).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--mode both|unfused|fused]
-                    [--no-cpu-baseline] [--kernel NAME --launches L] [--grid]
+                    [--no-cpu-baseline] [--kernel NAME --launches L] [--grid] [--configs]
 
 `value` is unfused DP cells/s = B*N*M / (fwd+bwd seconds); the fused figures ride along in
 the same line.  `roofline` covers the dominant kernel (largest share of a step), timed with
@@ -236,6 +236,94 @@ def run_grid(numerics):
     return 0
 
 
+def sinusoids(B, N, K, g):
+    """Normalize-config inputs: a sin(f t + phi) + N(0, 0.1), f ~ U[0.5, 3], phi ~ U[0, 2 pi],
+    a ~ U[0.5, 2] per (batch, feature)."""
+    import math
+
+    import torch
+
+    t = torch.linspace(0, 2 * math.pi, N).view(1, N, 1)
+    f = 0.5 + 2.5 * torch.rand(B, 1, K, generator=g)
+    ph = 2 * math.pi * torch.rand(B, 1, K, generator=g)
+    a = 0.5 + 1.5 * torch.rand(B, 1, K, generator=g)
+    return a * torch.sin(f * t + ph) + 0.1 * torch.randn(B, N, K, generator=g)
+
+
+def random_walks(Kseq, N, D, g):
+    """Barycenter-config inputs: cumsum of N(0, 0.1) steps plus a shared sinusoid template
+    sin(2 pi n / N (d + 1) / 2)."""
+    import math
+
+    import torch
+
+    n = torch.arange(N, dtype=torch.float32).view(N, 1)
+    d = torch.arange(D, dtype=torch.float32).view(1, D)
+    template = torch.sin(2 * math.pi * n / N * (d + 1) * 0.5)
+    return torch.cumsum(0.1 * torch.randn(Kseq, N, D, generator=g), dim=1) + template
+
+
+def run_configs(numerics):
+    """BASELINE.json configs 0, 2, 3, 4 on the GPU (config 1 is the default run): fwd+bwd
+    ms per step with fresh leaf clones (plumbing: loss .mean(); the others .sum()), and the
+    barycenter's 100 iterations end to end."""
+    import torch
+
+    from softdtw_cuda import SoftDTW, softdtw_barycenter
+
+    out = {}
+
+    def step_of(sdtw, X, Y, reduce):
+        def step():
+            xs = X.detach().clone().requires_grad_(True)
+            ys = Y.detach().clone().requires_grad_(True)
+            loss = sdtw(xs, ys)
+            (loss.mean() if reduce == "mean" else loss.sum()).backward()
+        return step
+
+    x, y = make_inputs(4, 64, 64, 8, seed=0)
+    ms, peak = time_steps(step_of(SoftDTW(gamma=1.0, fused=False), x.cuda(), y.cuda(), "mean"), 20, 3)
+    out["plumbing B=4 N=M=64 D=8 unfused"] = {"ms": round(ms, 4), "peak_mib": round(peak, 2)}
+    log(f"[configs] plumbing: {ms:.3f} ms")
+
+    x, y = make_inputs(16, 4096, 3072, 4, seed=0)
+    X, Y = x.cuda(), y.cuda()
+    for fused in (False, True):
+        ms, peak = time_steps(step_of(SoftDTW(gamma=0.1, fused=fused), X, Y, "sum"), 5, 1)
+        key = f"long B=16 N=4096 M=3072 D=4 gamma=0.1 {'fused' if fused else 'unfused'}"
+        out[key] = {"ms": round(ms, 3), "peak_mib": round(peak, 1),
+                    "cells_per_s": 16 * 4096 * 3072 / (ms * 1e-3)}
+        log(f"[configs] {key}: {ms:.3f} ms")
+    del X, Y
+    torch.cuda.empty_cache()
+
+    g = torch.Generator().manual_seed(0)
+    x = sinusoids(64, 256, 16, g)
+    y = sinusoids(64, 256, 16, g)
+    ms, peak = time_steps(step_of(SoftDTW(gamma=1.0, normalize=True, fused=True), x.cuda(),
+                                  y.cuda(), "sum"), 20, 3)
+    out["normalize B=64 N=M=256 D=16 fused"] = {"ms": round(ms, 4), "peak_mib": round(peak, 2)}
+    log(f"[configs] normalize: {ms:.3f} ms")
+
+    g = torch.Generator().manual_seed(0)
+    Xb = random_walks(64, 256, 8, g).cuda()
+    softdtw_barycenter(Xb, gamma=1.0, max_iter=2, lr=0.1, early_stopping=False)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    softdtw_barycenter(Xb, gamma=1.0, max_iter=100, lr=0.1, early_stopping=False)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3
+    out["barycenter K=64 N=256 D=8, 100 Adam iterations"] = {"ms": round(ms, 2),
+                                                              "ms_per_iteration": round(ms / 100, 4)}
+    log(f"[configs] barycenter: {ms:.1f} ms")
+
+    print(json.dumps({"metric": "fwd+bwd ms per step at the other BASELINE.json configs",
+                      "unit": "ms", "higher_is_better": False, "n_gpus": 1,
+                      "numerics": numerics, "dtype": "f32 (fp64 DP state)",
+                      "data": "synthetic (seed 0)", "configs": out}), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,6 +341,9 @@ def main(argv=None):
                     help="time the reference's benchmark grid (16 configurations, unfused and "
                          "fused, its protocol: one warm-up step, then the mean of 5) and print "
                          "one JSON line with the reference's figures beside ours")
+    ap.add_argument("--configs", action="store_true",
+                    help="time the other BASELINE.json configurations (plumbing, long "
+                         "sequences, normalize, barycenter) and print one JSON line")
     ap.add_argument("--numerics", choices=["mixed", "exact", "fast"], default="mixed",
                     help="cell arithmetic of the recursions (mixed, the default: forward "
                          "bit-identical to the reference CPU path, backward weights in fp32; "
@@ -275,6 +366,8 @@ def main(argv=None):
 
     if args.grid:
         return run_grid(args.numerics)
+    if args.configs:
+        return run_configs(args.numerics)
 
     B, N, M, K, gamma = 32, 512, 512, 64, 1.0
     cells = B * N * M

@@ -56,10 +56,33 @@ bool gamma_ok(double gamma) { return gamma > 0.0 && isfinite(gamma); }
 // ATen's naive bmm kernel (multiply, then add) runs when K*N*M < 400.
 bool small_bmm(int64_t N, int64_t M, int64_t K) { return K * N * M < 400; }
 
-// Bands per workgroup of the fused recursions: 2 where a producer wave per band computes the
-// matrix-core cost tiles (it needs a SIMD of its own: the fp32 matrix instructions take the
-// cycles of the SIMD they run on), else 4.
-int fused_wmax(int64_t N, int64_t M, int64_t K) { return (!small_bmm(N, M, K) && K <= 64) ? 2 : 4; }
+// Compute units of the current device (cached per device).
+int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+// Bands per workgroup of the fused recursions.  With matrix-core cost tiles a producer wave
+// per band computes them; it runs on a SIMD of its own (the fp32 matrix instructions take
+// the cycles of the SIMD they run on) when a workgroup holds 2 bands.  A 2-band workgroup
+// needs about 85 KiB of LDS, so one fits per CU: when the batch needs more 2-band
+// workgroups than there are CUs, the later pairs would wait for the earlier ones to finish,
+// and 4 bands per workgroup (producers sharing their compute waves' SIMDs, every
+// workgroup resident) finish sooner.  Scalar cost tiles always take 4.
+bool mfma_costs(int64_t N, int64_t M, int64_t K) { return !small_bmm(N, M, K) && K <= 64; }
+int fused_wmax(int64_t B, int64_t N, int64_t M, int64_t K) {
+    if (!mfma_costs(N, M, K)) return 4;
+    return B * dp_geom(N, 2).G <= cu_count() ? 2 : 4;
+}
+// workspace sizing: the 2-band geometry needs the most cross-workgroup rows
+int fused_ws_wmax(int64_t N, int64_t M, int64_t K) { return mfma_costs(N, M, K) ? 2 : 4; }
 
 // distance-backward split-reduction scratch: partials, then counters
 size_t ws_dist_bwd(int64_t B, int64_t N, int64_t M, int64_t K) {
@@ -206,9 +229,9 @@ size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) 
         case SDTW_OP_BWD:
             return ws_dp(B, N, M);
         case SDTW_OP_FUSED_FWD:
-            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_wmax(N, M, K));
+            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(N, M, K));
         case SDTW_OP_FUSED_BWD:
-            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_wmax(N, M, K)) + align_up(sizeof(float) * B * N * M) +
+            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(N, M, K)) + align_up(sizeof(float) * B * N * M) +
                    ws_dist_bwd(B, N, M, K);
         default:
             return 0;
@@ -317,7 +340,7 @@ int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const int wmax = fused_wmax(N, M, K);
+    const int wmax = fused_wmax(B, N, M, K);
     const DPScratch d = carve_dp(c, B, N, M, wmax);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess) return SDTW_ERR_LAUNCH;
@@ -339,7 +362,7 @@ static int fused_bwd_common(const float* x, const float* y, const float* R, cons
                             hipStream_t st) {
     if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess) return SDTW_ERR_LAUNCH;
     DPParams p{};
-    fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_wmax(N, M, K));
+    fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_wmax(B, N, M, K));
     p.x = x;
     p.y = y;
     p.x2 = x2;
@@ -362,7 +385,7 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const DPScratch d = carve_dp(c, B, N, M, fused_wmax(N, M, K));
+    const DPScratch d = carve_dp(c, B, N, M, fused_wmax(B, N, M, K));
     float* Ebuf = c.take<float>(B * N * M);
     float* part = c.take<float>(dist_bwd_split_floats(B, N, M, K));
     int* cnt = c.take<int>(dist_bwd_counters(B, N, M, K));
@@ -396,7 +419,7 @@ int sdtw_fused_bwd_e_f32(const float* x, const float* y, const float* R, const f
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const DPScratch d = carve_dp(c, B, N, M, fused_wmax(N, M, K));
+    const DPScratch d = carve_dp(c, B, N, M, fused_wmax(B, N, M, K));
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     return fused_bwd_common(x, y, R, gout, E, x2, y2, d, B, N, M, K, gamma, bandwidth,
                             (hipStream_t)stream);

@@ -780,13 +780,11 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
 
 // Waves of a workgroup: compute waves 0 .. W-1 (one band each) and the helper wave W; with
 // staged costs, the producer waves W .. 2W-1 (of bands 0 .. W-1) and the helper wave 2W.
-// Matrix-core producers run with W <= 2, so that under round-robin wave placement they take
-// the SIMDs the compute waves leave free; D producers (backward) share their compute wave's
-// SIMD (W <= 4).
+// With W = 2, matrix-core producers take the SIMDs the compute waves leave free under
+// round-robin wave placement; with W = 4 (large batches, see the launcher) every producer
+// shares its compute wave's SIMD, as D producers (backward) always do.
 template <class Cost, bool BWD>
-constexpr int dp_threads() {
-    return Produced<Cost, BWD>::value && std::is_same<Cost, CostD>::value ? 9 * WAVE : 5 * WAVE;
-}
+constexpr int dp_threads() { return Produced<Cost, BWD>::value ? 9 * WAVE : 5 * WAVE; }
 
 template <class Cost, bool BAND, bool EXACT>
 __global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPParams P) {

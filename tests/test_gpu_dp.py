@@ -167,8 +167,13 @@ def test_fused_feature_widths_match_unfused(K):
 
 @pytest.mark.parametrize("mode", MODES)
 def test_fused_matches_unfused_kernels(mode):
-    # fused recomputes the same cost bits: identical out / R / E
-    for (B, N, M, K) in [(3, 50, 40, 5), (2, 12, 9, 3), (2, 1100, 300, 4)]:
+    # fused recomputes the same cost bits: identical out / R / E.  The last two shapes need
+    # more 2-band workgroups than the GPU has CUs, so the fused launch takes 4 bands per
+    # workgroup (producers sharing their compute waves' SIMDs), one of them with
+    # cross-workgroup boundaries and a partial last workgroup.
+    for (B, N, M, K) in [(3, 50, 40, 5), (2, 12, 9, 3), (2, 1100, 300, 4), (300, 200, 150, 16),
+                         (70, 600, 100, 8)]:
+        say(f"[fused == unfused] mode={mode} B={B} N={N} M={M} K={K}")
         x, y = randn_pair(B, N, M, K, seed=N)
         xg, yg = x.cuda(), y.cuda()
         with numerics(mode):
