@@ -171,16 +171,17 @@ def test_fused_matches_unfused_kernels(mode):
     # more 2-band workgroups than the GPU has CUs, so the fused launch takes 4 bands per
     # workgroup (producers sharing their compute waves' SIMDs), one of them with
     # cross-workgroup boundaries and a partial last workgroup.
-    for (B, N, M, K) in [(3, 50, 40, 5), (2, 12, 9, 3), (2, 1100, 300, 4), (300, 200, 150, 16),
-                         (70, 600, 100, 8)]:
-        say(f"[fused == unfused] mode={mode} B={B} N={N} M={M} K={K}")
+    for (B, N, M, K, bw) in [(3, 50, 40, 5, -1.0), (2, 12, 9, 3, -1.0), (2, 1100, 300, 4, -1.0),
+                             (300, 200, 150, 16, -1.0), (70, 600, 100, 8, -1.0),
+                             (70, 600, 100, 8, 40.0)]:
+        say(f"[fused == unfused] mode={mode} B={B} N={N} M={M} K={K} bw={bw}")
         x, y = randn_pair(B, N, M, K, seed=N)
         xg, yg = x.cuda(), y.cuda()
         with numerics(mode):
             D = _engine.sqeuclid_fwd(xg, yg)
-            o1, R1 = _engine.dtw_fwd(D, 0.7, -1.0)
-            o2, R2 = _engine.fused_fwd(xg, yg, 0.7, -1.0)
-            E1 = _engine.dtw_bwd(D, R1, 0.7, -1.0)
-            E2 = _engine.fused_bwd_e(xg, yg, R2, 0.7, -1.0)
+            o1, R1 = _engine.dtw_fwd(D, 0.7, bw)
+            o2, R2 = _engine.fused_fwd(xg, yg, 0.7, bw)
+            E1 = _engine.dtw_bwd(D, R1, 0.7, bw)
+            E2 = _engine.fused_bwd_e(xg, yg, R2, 0.7, bw)
         assert torch.equal(o1, o2) and torch.equal(R1, R2)
         assert torch.equal(E1, E2)
