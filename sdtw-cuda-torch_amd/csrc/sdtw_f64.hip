@@ -196,6 +196,119 @@ __global__ void __launch_bounds__(kSweepThreads) dp_bwd_kernel(const double* __r
     }
 }
 
+// The same recursions with the rolling anti-diagonals in LDS: the values of diagonals d - 1
+// and d - 2 (forward) or d + 1 and d + 2 (backward), indexed by row over the padded table
+// (row 0 .. N + 1), are read from LDS instead of global memory.  Each sweep visits every
+// padded entry of its diagonals, so every neighbour read lands on an entry written one or
+// two diagonals earlier.  The forward writes every entry of R, the backward every cell of G
+// (gout * E, 0 out of the band), so neither needs an initialising or scaling pass.
+constexpr int64_t kLdsBytes = 160 * 1024;
+inline int64_t fwd_lds_bytes(int64_t N) { return 3 * (N + 2) * (int64_t)sizeof(double); }
+inline int64_t bwd_lds_bytes(int64_t N) { return 9 * (N + 2) * (int64_t)sizeof(double); }
+
+__global__ void __launch_bounds__(kSweepThreads) dp_fwd_lds_kernel(const double* __restrict__ Dall,
+                                                                   double* __restrict__ Rall,
+                                                                   double* __restrict__ out, int N,
+                                                                   int M, double gamma, double bw) {
+    extern __shared__ double sh[];
+    const int64_t b = blockIdx.x;
+    const int64_t W = M + 2;
+    double* R = Rall + b * (N + 2) * W;
+    const double* D = Dall + b * N * M;
+    const double INF = __builtin_inf();
+    const int L = N + 2;
+    for (int d = 0; d <= N + M + 2; ++d) {
+        double* cur = sh + (d % 3) * L;
+        const double* p1 = sh + ((d + 2) % 3) * L;  // diagonal d - 1
+        const double* p2 = sh + ((d + 1) % 3) * L;  // diagonal d - 2
+        const int ilo = d - (M + 1) > 0 ? d - (M + 1) : 0;
+        const int ihi = d < N + 1 ? d : N + 1;
+        for (int i = ilo + threadIdx.x; i <= ihi; i += blockDim.x) {
+            const int j = d - i;
+            double v;
+            if (i == 0 || j == 0) {
+                v = (i == 0 && j == 0) ? 0.0 : INF;
+            } else if (i > N || j > M || out_of_band(bw, i, j)) {
+                v = INF;
+            } else {
+                const double r0 = -p2[i - 1] / gamma;  // (i-1, j-1)
+                const double r1 = -p1[i - 1] / gamma;  // (i-1, j)
+                const double r2 = -p1[i] / gamma;      // (i, j-1)
+                double rmax = (r1 > r0) ? r1 : r0;
+                rmax = (r2 > rmax) ? r2 : rmax;
+                const double rsum = exp(r0 - rmax) + exp(r1 - rmax) + exp(r2 - rmax);
+                const double softmin = -gamma * (log(rsum) + rmax);
+                v = D[(int64_t)(i - 1) * M + (j - 1)] + softmin;
+            }
+            cur[i] = v;
+            R[i * W + j] = v;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[b] = R[N * W + M];
+}
+
+__global__ void __launch_bounds__(kSweepThreads) dp_bwd_lds_kernel(const double* __restrict__ Dall,
+                                                                   const double* __restrict__ Rall,
+                                                                   const double* __restrict__ gout,
+                                                                   double* __restrict__ Gall, int N,
+                                                                   int M, double gamma, double bw) {
+    extern __shared__ double sh[];
+    const int64_t b = blockIdx.x;
+    const int64_t W = M + 2;
+    const double* R = Rall + b * (N + 2) * W;
+    const double* D = Dall + b * N * M;
+    double* G = Gall + b * N * M;
+    const double NINF = -__builtin_inf();
+    const double corner = R[N * W + M];
+    const double g = gout ? gout[b] : 1.0;
+    const int L = N + 2;
+    // buffers k = 0, 1, 2 of E, R (its +inf read as -inf) and D, by row
+    auto Eb = [&](int k) { return sh + k * L; };
+    auto Rb = [&](int k) { return sh + (3 + k) * L; };
+    auto Db = [&](int k) { return sh + (6 + k) * L; };
+    for (int d = N + M + 2; d >= 2; --d) {
+        const int k0 = d % 3, k1 = (d + 1) % 3, k2 = (d + 2) % 3;  // diagonals d, d+1, d+2
+        double *Ec = Eb(k0), *Rc = Rb(k0), *Dc = Db(k0);
+        const double *E1 = Eb(k1), *R1 = Rb(k1), *D1 = Db(k1);
+        const double *E2 = Eb(k2), *R2 = Rb(k2), *D2 = Db(k2);
+        const int ilo = d - (M + 1) > 1 ? d - (M + 1) : 1;
+        const int ihi = d - 1 < N + 1 ? d - 1 : N + 1;
+        for (int i = ilo + threadIdx.x; i <= ihi; i += blockDim.x) {
+            const int j = d - i;
+            double e, r, dv;
+            if (i == N + 1 || j == M + 1) {
+                const bool c = (i == N + 1 && j == M + 1);
+                e = c ? 1.0 : 0.0;
+                r = c ? corner : NINF;
+                dv = 0.0;
+            } else {
+                const double rv = R[i * W + j];
+                r = isinf(rv) ? NINF : rv;
+                dv = D[(int64_t)(i - 1) * M + (j - 1)];
+                e = 0.0;
+                if (!out_of_band(bw, i, j)) {
+                    const double da = (R1[i + 1] - r) - D1[i + 1];  // (i+1, j)
+                    const double db = (R1[i] - r) - D1[i];          // (i, j+1)
+                    const double dc = (R2[i + 1] - r) - D2[i + 1];  // (i+1, j+1)
+                    const double a = exp(da / gamma);
+                    const double bb = exp(db / gamma);
+                    const double cc = exp(dc / gamma);
+                    double acc = E1[i + 1] * a;
+                    acc = acc + E1[i] * bb;
+                    acc = acc + E2[i + 1] * cc;
+                    e = acc;
+                }
+                G[(int64_t)(i - 1) * M + (j - 1)] = g * e;
+            }
+            Ec[i] = e;
+            Rc[i] = r;
+            Dc[i] = dv;
+        }
+        __syncthreads();
+    }
+}
+
 bool shape_ok(int64_t B, int64_t N, int64_t M, int64_t K, bool need_k) {
     if (B < 0 || N <= 0 || M <= 0 || B > 65535) return false;
     if (need_k && (K <= 0 || K > INT32_MAX)) return false;
@@ -253,8 +366,18 @@ int sdtw_fwd_f64(const double* D, double* R, double* out, int64_t B, int64_t N, 
     if (!(gamma > 0.0) || !isfinite(gamma)) return SDTW_ERR_INVALID_VALUE;
     if (B == 0) return SDTW_OK;
     if (!D || !R || !out) return SDTW_ERR_INVALID_VALUE;
-    hipLaunchKernelGGL(dp_fwd_kernel, dim3((unsigned)B), dim3(kSweepThreads), 0,
-                       (hipStream_t)stream, D, R, out, (int)N, (int)M, gamma, bandwidth);
+    const int64_t lds = fwd_lds_bytes(N);
+    if (lds <= kLdsBytes) {
+        if (lds > 64 * 1024 &&
+            hipFuncSetAttribute(reinterpret_cast<const void*>(dp_fwd_lds_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return SDTW_ERR_LAUNCH;
+        hipLaunchKernelGGL(dp_fwd_lds_kernel, dim3((unsigned)B), dim3(kSweepThreads), (size_t)lds,
+                           (hipStream_t)stream, D, R, out, (int)N, (int)M, gamma, bandwidth);
+    } else {
+        hipLaunchKernelGGL(dp_fwd_kernel, dim3((unsigned)B), dim3(kSweepThreads), 0,
+                           (hipStream_t)stream, D, R, out, (int)N, (int)M, gamma, bandwidth);
+    }
     return status_of(hipGetLastError());
 }
 
@@ -264,8 +387,18 @@ int sdtw_bwd_f64(const double* D, const double* R, const double* gout, double* G
     if (!(gamma > 0.0) || !isfinite(gamma)) return SDTW_ERR_INVALID_VALUE;
     if (B == 0) return SDTW_OK;
     if (!D || !R || !G) return SDTW_ERR_INVALID_VALUE;
-    hipLaunchKernelGGL(dp_bwd_kernel, dim3((unsigned)B), dim3(kSweepThreads), 0,
-                       (hipStream_t)stream, D, R, gout, G, (int)N, (int)M, gamma, bandwidth);
+    const int64_t lds = bwd_lds_bytes(N);
+    if (lds <= kLdsBytes) {
+        if (lds > 64 * 1024 &&
+            hipFuncSetAttribute(reinterpret_cast<const void*>(dp_bwd_lds_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return SDTW_ERR_LAUNCH;
+        hipLaunchKernelGGL(dp_bwd_lds_kernel, dim3((unsigned)B), dim3(kSweepThreads), (size_t)lds,
+                           (hipStream_t)stream, D, R, gout, G, (int)N, (int)M, gamma, bandwidth);
+    } else {
+        hipLaunchKernelGGL(dp_bwd_kernel, dim3((unsigned)B), dim3(kSweepThreads), 0,
+                           (hipStream_t)stream, D, R, gout, G, (int)N, (int)M, gamma, bandwidth);
+    }
     return status_of(hipGetLastError());
 }
 

@@ -57,6 +57,8 @@ CASES = [
     (1, 1, 1, 2, 1.0, None),
     (2, 1, 7, 2, 1.0, None),
     (2, 7, 1, 2, 0.5, None),
+    (1, 3000, 40, 2, 0.5, 100.0),     # backward diagonals beyond LDS: global-memory sweep
+    (1, 7000, 20, 2, 1.0, None),      # forward diagonals beyond LDS too
 ]
 
 
