@@ -16,9 +16,9 @@
 // N+1 / column M+1 read by the backward).  One workgroup owns a pair and sweeps it by
 // anti-diagonals: the cells of a diagonal are independent, so its threads compute them at
 // once and a workgroup barrier separates consecutive diagonals.  There are no waits between
-// workgroups.  The neighbours are read back from global memory (the workgroup's own writes,
-// made visible by the barrier), so any N and M fit.  This path favours a direct restatement
-// over speed: it exists so that float64 callers get float64 results.
+// workgroups.  The last diagonals live in LDS; where they do not fit, the same sweep reads
+// its neighbours back from global memory (the workgroup's own writes, made visible by the
+// barrier), so any N and M fit.  The distance kernels are LDS-tiled.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -32,29 +32,6 @@ constexpr int kSweepThreads = 1024;
 __device__ __forceinline__ bool out_of_band(double bw, int64_t i, int64_t j) {
     const int64_t d = i > j ? i - j : j - i;
     return 0.0 < bw && bw < (double)d;
-}
-
-// D[b,i,j] = max(0, (|x_i|^2 + |y_j|^2) - 2 x_i.y_j), the operation order of
-// distances.py:20-25 (norms and dot as sequential sums).  One thread per cell.
-__global__ void __launch_bounds__(256) dist_fwd_kernel(const double* __restrict__ x,
-                                                       const double* __restrict__ y,
-                                                       double* __restrict__ D, int N, int M,
-                                                       int K) {
-    const int j = blockIdx.x * 64 + (threadIdx.x & 63);
-    const int i = blockIdx.y * 4 + (threadIdx.x >> 6);
-    const int64_t b = blockIdx.z;
-    if (i >= N || j >= M) return;
-    const double* xi = x + (b * N + i) * K;
-    const double* yj = y + (b * M + j) * K;
-    double x2 = 0.0, y2 = 0.0, dot = 0.0;
-    for (int k = 0; k < K; ++k) {
-        const double a = xi[k], c = yj[k];
-        x2 = fma(a, a, x2);
-        y2 = fma(c, c, y2);
-        dot = fma(a, c, dot);
-    }
-    const double pre = (x2 + y2) - 2.0 * dot;
-    D[(b * N + i) * M + j] = pre > 0.0 ? pre : (pre == pre ? 0.0 : pre);
 }
 
 // clamp_min's backward passes the gradient where the pre-clamp value is >= 0: every cell with
@@ -74,36 +51,135 @@ __device__ __forceinline__ double masked(double g, double d, const double* xi, c
     return ((x2 + y2) - 2.0 * dot) >= 0.0 ? g : 0.0;
 }
 
-// gx[b,i,k] = 2 x[b,i,k] sum_j G'[b,i,j] - 2 sum_j G'[b,i,j] y[b,j,k]  (TRANS = false), and
-// gy[b,j,k] = 2 y[b,j,k] sum_i G'[b,i,j] - 2 sum_i G'[b,i,j] x[b,i,k]  (TRANS = true).
-// One thread per output element: 64 features of 4 output rows per block.
-template <bool TRANS>
-__global__ void __launch_bounds__(256) dist_bwd_kernel(const double* __restrict__ x,
-                                                       const double* __restrict__ y,
-                                                       const double* __restrict__ D,
-                                                       const double* __restrict__ G,
-                                                       double* __restrict__ out, int N, int M,
-                                                       int K, int mask) {
-    const int k = blockIdx.x * 64 + (threadIdx.x & 63);
-    const int r = blockIdx.y * 4 + (threadIdx.x >> 6);  // output row: i (gx) or j (gy)
+// The distance and its backward, tiled: a block of 256 threads owns a 64 x 64 output tile,
+// each thread 4 x 4 outputs strided by 16 (conflict-free LDS reads), and the reduction runs
+// in chunks of 16 staged through LDS.  Every output is one sequential sum over the reduction
+// index (the operation order of distances.py:20-25: norms and dot accumulated over k, then
+// (x2 + y2) - 2 dot, clamped at 0):
+//   D[b,i,j]  = max(0, (|x_i|^2 + |y_j|^2) - 2 x_i.y_j)
+//   gx[b,i,k] = 2 x[b,i,k] sum_j G'[b,i,j] - 2 sum_j G'[b,i,j] y[b,j,k]   (TRANS = false)
+//   gy[b,j,k] = 2 y[b,j,k] sum_i G'[b,i,j] - 2 sum_i G'[b,i,j] x[b,i,k]   (TRANS = true)
+constexpr int kT = 64, kKC = 16;
+
+// D tile: rows i0 .. i0 + 63 of x, columns j0 .. j0 + 63 (rows of y); norms and dots
+// accumulated over k in order.
+__global__ void __launch_bounds__(256) dist_fwd_tiled_kernel(const double* __restrict__ x,
+                                                             const double* __restrict__ y,
+                                                             double* __restrict__ D, int N, int M,
+                                                             int K) {
+    __shared__ double xs[kKC][kT + 1], ys[kKC][kT + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int i0 = blockIdx.y * kT, j0 = blockIdx.x * kT;
     const int64_t b = blockIdx.z;
-    const int R = TRANS ? M : N, T = TRANS ? N : M;     // output rows, reduction length
-    if (r >= R) return;
-    const double* self = (TRANS ? y + (b * M + r) * K : x + (b * N + r) * K);
+    const double* xb = x + b * N * K;
+    const double* yb = y + b * M * K;
+    double dot[4][4] = {}, x2[4] = {}, y2[4] = {};
+    for (int k0 = 0; k0 < K; k0 += kKC) {
+        // 64 rows x 16 features of x and of y: 4 of each per thread, zero past the edges
+        for (int e = threadIdx.x; e < kT * kKC; e += 256) {
+            const int r = e / kKC, kk = e % kKC, k = k0 + kk;
+            xs[kk][r] = (i0 + r < N && k < K) ? xb[(int64_t)(i0 + r) * K + k] : 0.0;
+            ys[kk][r] = (j0 + r < M && k < K) ? yb[(int64_t)(j0 + r) * K + k] : 0.0;
+        }
+        __syncthreads();
+        const int kn = K - k0 < kKC ? K - k0 : kKC;
+        for (int kk = 0; kk < kn; ++kk) {
+            double a[4], c[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                a[u] = xs[kk][ty + 16 * u];
+                c[u] = ys[kk][tx + 16 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                x2[u] = fma(a[u], a[u], x2[u]);
+                y2[u] = fma(c[u], c[u], y2[u]);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) dot[u][v] = fma(a[u], c[v], dot[u][v]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = i0 + ty + 16 * u;
+        if (i >= N) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int j = j0 + tx + 16 * v;
+            if (j >= M) continue;
+            const double pre = (x2[u] + y2[v]) - 2.0 * dot[u][v];
+            D[(b * N + i) * M + j] = pre > 0.0 ? pre : (pre == pre ? 0.0 : pre);
+        }
+    }
+}
+
+// gx (TRANS = false): 64 output rows i x 64 features k, reduction over j; gy (TRANS = true):
+// rows j, reduction over i.  The masked G tile (rows x 16 reduction indices) and the 16 x 64
+// feature tile of the other operand are staged per chunk; every thread sums its rows' G'
+// from LDS in order, as the simple kernel does.
+template <bool TRANS>
+__global__ void __launch_bounds__(256) dist_bwd_tiled_kernel(const double* __restrict__ x,
+                                                             const double* __restrict__ y,
+                                                             const double* __restrict__ D,
+                                                             const double* __restrict__ G,
+                                                             double* __restrict__ out, int N,
+                                                             int M, int K, int mask) {
+    __shared__ double gs[kKC][kT + 1], os[kKC][kT + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int r0 = blockIdx.y * kT, k0 = blockIdx.x * kT;
+    const int64_t b = blockIdx.z;
+    const int R = TRANS ? M : N, T = TRANS ? N : M;
+    const double* selfb = TRANS ? y + b * M * K : x + b * N * K;
     const double* other = TRANS ? x + b * N * K : y + b * M * K;
     const double* Gb = G + b * N * M;
-    const double* Db = mask ? D + b * N * M : nullptr;  // D is not passed without the mask
-    const bool kin = k < K;
-    double s = 0.0, acc = 0.0;
-    for (int t = 0; t < T; ++t) {
-        const int64_t cell = TRANS ? (int64_t)t * M + r : (int64_t)r * M + t;
-        const double* xi = TRANS ? other + (int64_t)t * K : self;
-        const double* yj = TRANS ? self : other + (int64_t)t * K;
-        const double g = Db ? masked(Gb[cell], Db[cell], xi, yj, K) : Gb[cell];
-        s += g;
-        if (kin) acc = fma(g, other[(int64_t)t * K + k], acc);
+    const double* Db = mask ? D + b * N * M : nullptr;
+    double acc[4][4] = {}, s[4] = {};
+    for (int t0 = 0; t0 < T; t0 += kKC) {
+        for (int e = threadIdx.x; e < kT * kKC; e += 256) {
+            // G' tile: consecutive threads along G's rows (j for gy, the reduction index t
+            // for gx), so that they read consecutive entries
+            const int r = TRANS ? e % kT : e / kKC, tt = TRANS ? e / kT : e % kKC, t = t0 + tt;
+            double g = 0.0;
+            if (r0 + r < R && t < T) {
+                const int64_t cell = TRANS ? (int64_t)t * M + (r0 + r) : (int64_t)(r0 + r) * M + t;
+                const double* xi = TRANS ? other + (int64_t)t * K : selfb + (int64_t)(r0 + r) * K;
+                const double* yj = TRANS ? selfb + (int64_t)(r0 + r) * K : other + (int64_t)t * K;
+                g = Db ? masked(Gb[cell], Db[cell], xi, yj, K) : Gb[cell];
+            }
+            gs[tt][r] = g;
+            const int ft = e / kT, kk = e % kT;  // feature tile: 16 reduction rows x 64 features
+            os[ft][kk] = (t0 + ft < T && k0 + kk < K) ? other[(int64_t)(t0 + ft) * K + k0 + kk] : 0.0;
+        }
+        __syncthreads();
+        const int tn = T - t0 < kKC ? T - t0 : kKC;
+        for (int tt = 0; tt < tn; ++tt) {
+            double g[4], o[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                g[u] = gs[tt][ty + 16 * u];
+                o[u] = os[tt][tx + 16 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                s[u] += g[u];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[u][v] = fma(g[u], o[v], acc[u][v]);
+            }
+        }
+        __syncthreads();
     }
-    if (kin) out[(b * R + r) * K + k] = 2.0 * s * self[k] - 2.0 * acc;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int r = r0 + ty + 16 * u;
+        if (r >= R) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int k = k0 + tx + 16 * v;
+            if (k >= K) continue;
+            out[(b * R + r) * K + k] = 2.0 * s[u] * selfb[(int64_t)r * K + k] - 2.0 * acc[u][v];
+        }
+    }
 }
 
 // Forward recursion of pair blockIdx.x (launcher.py:307-324), R (N+2, M+2) dense.
@@ -336,8 +412,8 @@ int sdtw_sqeuclid_fwd_f64(const double* x, const double* y, double* D, int64_t B
     if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
     if (B == 0) return SDTW_OK;
     if (!x || !y || !D) return SDTW_ERR_INVALID_VALUE;
-    hipLaunchKernelGGL(dist_fwd_kernel, dim3((unsigned)((M + 63) / 64), (unsigned)((N + 3) / 4),
-                                             (unsigned)B),
+    hipLaunchKernelGGL(dist_fwd_tiled_kernel,
+                       dim3((unsigned)((M + kT - 1) / kT), (unsigned)((N + kT - 1) / kT), (unsigned)B),
                        dim3(256), 0, (hipStream_t)stream, x, y, D, (int)N, (int)M, (int)K);
     return status_of(hipGetLastError());
 }
@@ -350,12 +426,12 @@ int sdtw_sqeuclid_bwd_f64(const double* x, const double* y, const double* D, con
     if (!x || !y || !G || !gx || !gy || (mask && !D)) return SDTW_ERR_INVALID_VALUE;
     if ((K + 63) / 64 > INT32_MAX) return SDTW_ERR_UNSUPPORTED;
     const hipStream_t st = (hipStream_t)stream;
-    const unsigned kb = (unsigned)((K + 63) / 64);
-    hipLaunchKernelGGL(dist_bwd_kernel<false>, dim3(kb, (unsigned)((N + 3) / 4), (unsigned)B),
+    const unsigned kb = (unsigned)((K + kT - 1) / kT);
+    hipLaunchKernelGGL(dist_bwd_tiled_kernel<false>, dim3(kb, (unsigned)((N + kT - 1) / kT), (unsigned)B),
                        dim3(256), 0, st, x, y, D, G, gx, (int)N, (int)M, (int)K, mask);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return SDTW_ERR_LAUNCH;
-    hipLaunchKernelGGL(dist_bwd_kernel<true>, dim3(kb, (unsigned)((M + 3) / 4), (unsigned)B),
+    hipLaunchKernelGGL(dist_bwd_tiled_kernel<true>, dim3(kb, (unsigned)((M + kT - 1) / kT), (unsigned)B),
                        dim3(256), 0, st, x, y, D, G, gy, (int)N, (int)M, (int)K, mask);
     return status_of(hipGetLastError());
 }
