@@ -173,7 +173,8 @@ def test_fused_matches_unfused_kernels(mode):
     # cross-workgroup boundaries and a partial last workgroup.
     for (B, N, M, K, bw) in [(3, 50, 40, 5, -1.0), (2, 12, 9, 3, -1.0), (2, 1100, 300, 4, -1.0),
                              (300, 200, 150, 16, -1.0), (70, 600, 100, 8, -1.0),
-                             (70, 600, 100, 8, 40.0)]:
+                             (70, 600, 100, 8, 40.0), (2, 1, 7, 3, -1.0), (2, 7, 1, 3, -1.0),
+                             (1, 65, 1, 2, -1.0)]:
         say(f"[fused == unfused] mode={mode} B={B} N={N} M={M} K={K} bw={bw}")
         x, y = randn_pair(B, N, M, K, seed=N)
         xg, yg = x.cuda(), y.cuda()
