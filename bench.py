@@ -73,6 +73,7 @@ def algorithmic_bytes(kernel, B, N, M, K):
         "dp_bwd": 4 * (3 * cells),             # read D, R; write G
         "dist_bwd": 4 * (cells + 2 * xy),      # read G, x, y; write gx, gy
         "fused_fwd": 4 * (cells + xy),         # read x, y; write R
+        "fused_fwd_d": 4 * (2 * cells + xy),   # read x, y; write D, R
         "fused_bwd_e": 4 * (2 * cells + xy),   # read R, x, y; write g*E
     }[kernel]
 
@@ -101,6 +102,7 @@ def kernel_launcher(name, xg, yg, gamma):
         "dp_bwd": lambda: _engine.dtw_bwd(D, R, gamma, -1.0),
         "dist_bwd": lambda: _engine.sqeuclid_bwd(xg, yg, D, G, mask=True),
         "fused_fwd": lambda: _engine.fused_fwd(xg, yg, gamma, -1.0),
+        "fused_fwd_d": lambda: _engine.fused_fwd_d(xg, yg, gamma, -1.0),
         "fused_bwd_e": lambda: _engine.fused_bwd_e(xg, yg, R, gamma, -1.0),
     }[name]
     return fn
@@ -333,7 +335,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", default=None,
                     help="only launch one kernel family repeatedly (for rocprofv3 runs): "
-                         "dist_fwd, dp_fwd, dp_bwd, dist_bwd, fused_fwd, fused_bwd_e, copy")
+                         "dist_fwd, dp_fwd, dp_bwd, dist_bwd, fused_fwd, fused_fwd_d, fused_bwd_e, copy")
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--shape", default=None,
                     help="B,N,M,D for --kernel runs (default: the headline 32,512,512,64)")
@@ -407,8 +409,12 @@ def main(argv=None):
 
     # per-kernel timing (HIP events on the engine's stream) -> dominant kernel roofline
     kernels = []
+    # unfused mode's forward: one launch forming D and R (fused_fwd_d), except under "fast"
+    # arithmetic, where the module keeps the distance and the recursion apart
+    unfused_kernels = (["dist_fwd", "dp_fwd", "dp_bwd", "dist_bwd"] if args.numerics == "fast"
+                       else ["fused_fwd_d", "dp_bwd", "dist_bwd"])
     if "unfused" in res:
-        kernels += ["dist_fwd", "dp_fwd", "dp_bwd", "dist_bwd"]
+        kernels += unfused_kernels
     if "fused" in res:
         kernels += ["fused_fwd", "fused_bwd_e"]
     per = {}
@@ -417,8 +423,7 @@ def main(argv=None):
         per[kname] = time_kernel(fn, max(5, min(args.steps, 20)))
         log(f"[bench] kernel {kname}: {per[kname]:.4f} ms/launch")
     head_mode = "unfused" if "unfused" in res else "fused"
-    head_kernels = {"unfused": ["dist_fwd", "dp_fwd", "dp_bwd", "dist_bwd"],
-                    "fused": ["fused_fwd", "fused_bwd_e"]}[head_mode]
+    head_kernels = {"unfused": unfused_kernels, "fused": ["fused_fwd", "fused_bwd_e"]}[head_mode]
     dom = max(head_kernels, key=per.get)  # dominant kernel of the step `value` measures
     abytes = algorithmic_bytes(dom, B, N, M, K)
     achieved = abytes / (per[dom] * 1e-3) / 1e9

@@ -151,6 +151,15 @@ int sdtw_fused_fwd_f32(const float *x, const float *y, float *R, float *out, int
                        int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
                        void *ws, size_t ws_bytes, void *stream);
 
+/* Unfused mode's forward in one launch: the fused forward whose matrix-core producer waves
+ * also store every cost tile into D (B,N,M), with the bits sdtw_sqeuclid_fwd_f32(EXACT)
+ * writes.  Replaces distances.py:6-28 followed by launcher.py:167-223 (the cost tensor,
+ * then the recursion over it).  Workspace as SDTW_OP_FUSED_FWD.  SDTW_ERR_UNSUPPORTED
+ * where the costs take scalar tiles (K > 64, or K*N*M < 400): use the two calls there. */
+int sdtw_fused_fwd_d_f32(const float *x, const float *y, float *D, float *R, float *out,
+                         int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
+                         double bandwidth, void *ws, size_t ws_bytes, void *stream);
+
 /* Fused backward: E recomputed with per-cell costs from x, y, then
  *   gx = 2 (x * rowsum(gE) - gE y),  gy = 2 (y * colsum(gE) - gE^T x),  gE = gout[b] * E.
  * gout may be NULL (treated as 1).  E lives only in the workspace.

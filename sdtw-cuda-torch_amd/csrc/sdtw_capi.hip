@@ -330,9 +330,11 @@ int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, in
     return status_of(launch_bwd(p, false, false, exact_backward(), (hipStream_t)stream));
 }
 
-int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int64_t B,
-                       int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
-                       void* ws, size_t ws_bytes, void* stream) {
+// Fused forward; with D non-null the matrix-core producer waves also store each cost tile
+// into D (B,N,M).
+static int fused_fwd_common(const float* x, const float* y, float* D, float* R, float* out,
+                            int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
+                            double bandwidth, void* ws, size_t ws_bytes, void* stream) {
     if (!shape_ok(B, N, M, K, true) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
     if (B == 0) return SDTW_OK;
     if (!x || !y || !R || !out) return SDTW_ERR_INVALID_VALUE;
@@ -352,7 +354,24 @@ int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int
     p.y2 = y2;
     p.R = R;
     p.out = out;
+    p.D_out = D;
     return status_of(launch_fwd(p, true, small_bmm(N, M, K), exact_forward(), st));
+}
+
+int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int64_t B,
+                       int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
+                       void* ws, size_t ws_bytes, void* stream) {
+    return fused_fwd_common(x, y, nullptr, R, out, B, N, M, K, gamma, bandwidth, ws, ws_bytes,
+                            stream);
+}
+
+int sdtw_fused_fwd_d_f32(const float* x, const float* y, float* D, float* R, float* out,
+                         int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
+                         double bandwidth, void* ws, size_t ws_bytes, void* stream) {
+    if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
+    if (!mfma_costs(N, M, K)) return SDTW_ERR_UNSUPPORTED;  // scalar cost tiles: no producer
+    if (B > 0 && !D) return SDTW_ERR_INVALID_VALUE;
+    return fused_fwd_common(x, y, D, R, out, B, N, M, K, gamma, bandwidth, ws, ws_bytes, stream);
 }
 
 // Fused backward core: norms, then the reverse wavefront writing gout * E into `E`.

@@ -378,6 +378,20 @@ struct CostMfma {
             for (int r = 0; r < 4; ++r)
                 dst[(16 * rb + r) * CS] = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
     }
+    // the same tile into the pair's cost tensor Dp (N, M): lane l's column c0 + (l & 15) of
+    // rows row0 + 16 rb + 4 (l >> 4) + r, 16 lanes per 64-byte row segment
+    SDTW_DEV void store_d(float* Dp, int c0, int row0, int N) const {
+        const int l = threadIdx.x & (WAVE - 1);
+        const int col = c0 + (l & 15);
+        if ((unsigned)col >= (unsigned)M) return;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = row0 + 16 * rb + 4 * (l >> 4) + r;
+                if (row < N) Dp[(int64_t)row * M + col] = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
+            }
+    }
 };
 
 // Fused fallback (features beyond the register-resident width, and the tiny problems whose
@@ -582,6 +596,11 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
         else c.store(ring, col(t));
         if ((threadIdx.x & (WAVE - 1)) == 0) lds_publish(ready, t + 1);
         if (t + 1 < T) c.issue(col(t + 1));
+        // unfused mode's cost tensor, from the same tile (forward; after the next loads, so
+        // that they do not queue behind these stores)
+        if constexpr (MMA && !BWD) {
+            if (P.D_out) c.store_d(P.D_out + (int64_t)p * P.N * P.M, col(t), b * WAVE, P.N);
+        }
         if (flush) gt.write(P, p, b);
     }
     if (BWD) {

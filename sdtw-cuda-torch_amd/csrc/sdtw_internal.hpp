@@ -17,6 +17,7 @@ struct DPParams {
     float* out;         // (B) forward result
     float* G_out;       // backward: (B,N,M) = gout * E
     const float* gout;  // backward: (B) upstream gradient or nullptr (= 1)
+    float* D_out;       // fused forward: the cost tiles also stored here (B,N,M), or nullptr
     int* ticket;        // workgroup ticket counter (zeroed by the prep kernel)
     double* gring;      // forward: (B*G, RW) fp64 last rows of each workgroup's bands
     float4* gring4;     // backward: (B*G, RW) (E, R, D, tag) first rows

@@ -50,6 +50,9 @@ _SIGS = {
     "sdtw_fused_fwd_f32": ([ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4
                            + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                            ctypes.c_int),
+    "sdtw_fused_fwd_d_f32": ([ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4
+                             + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+                             ctypes.c_int),
     "sdtw_fused_bwd_f32": ([ctypes.c_void_p] * 6 + [ctypes.c_int64] * 4
                            + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                            ctypes.c_int),
@@ -301,6 +304,33 @@ def fused_fwd(x, y, gamma: float, bandwidth: float):
     _check(rc, "fused forward")
     _debug_check(OP_FUSED_FWD, ws, nws, B, N, M, K, "fused forward")
     return out, R
+
+
+def fused_costs_on_matrix_cores(N: int, M: int, K: int) -> bool:
+    """Whether the fused recursions take their cost tiles from matrix-core producer waves
+    (K <= 64 and K*N*M >= 400: the shapes whose reference dot is a fused multiply-add
+    chain), which sdtw_fused_fwd_d_f32 needs."""
+    return K <= 64 and K * N * M >= 400
+
+
+def fused_fwd_d(x, y, gamma: float, bandwidth: float):
+    """Unfused mode's forward in one launch: (out, R, D) with D the (B,N,M) cost tensor."""
+    require_gpu(x, "fused forward x")
+    require_gpu(y, "fused forward y")
+    _check_shapes(x=x, y=y)
+    B, N, K = x.shape
+    M = y.shape[1]
+    D = torch.empty((B, N, M), dtype=torch.float32, device=x.device)
+    R = torch.empty((table_elems(B, N, M),), dtype=torch.float32, device=x.device)
+    out = torch.empty((B,), dtype=torch.float32, device=x.device)
+    ws, nws = _workspace(OP_FUSED_FWD, B, N, M, K, x.device)
+    with torch.cuda.device(x.device):
+        rc = load().sdtw_fused_fwd_d_f32(_ptr(x), _ptr(y), _ptr(D), _ptr(R), _ptr(out), B, N, M,
+                                         K, float(gamma), float(bandwidth), _ptr(ws), nws,
+                                         _stream(x.device))
+    _check(rc, "fused forward (with D)")
+    _debug_check(OP_FUSED_FWD, ws, nws, B, N, M, K, "fused forward (with D)")
+    return out, R, D
 
 
 def fused_bwd(x, y, R, gamma: float, bandwidth: float, gout=None):

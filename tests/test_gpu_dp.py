@@ -186,3 +186,36 @@ def test_fused_matches_unfused_kernels(mode):
             E2 = _engine.fused_bwd_e(xg, yg, R2, 0.7, bw)
         assert torch.equal(o1, o2) and torch.equal(R1, R2)
         assert torch.equal(E1, E2)
+
+
+@pytest.mark.parametrize("B,N,M,K,bw", [(3, 100, 80, 16, -1.0), (2, 130, 70, 64, 20.0),
+                                        (300, 200, 150, 16, -1.0), (70, 600, 100, 8, 40.0)])
+def test_unfused_one_launch_forward_matches_two_calls(B, N, M, K, bw):
+    # D from the fused forward's producers has the distance kernel's bits, and R / out are the
+    # recursion over it (2-band and 4-band fused geometries, with and without a band)
+    say(f"[one-launch unfused forward] B={B} N={N} M={M} K={K} bw={bw}")
+    x, y = randn_pair(B, N, M, K, seed=N)
+    xg, yg = x.cuda(), y.cuda()
+    D1 = _engine.sqeuclid_fwd(xg, yg)
+    o1, R1 = _engine.dtw_fwd(D1, 0.7, bw)
+    o2, R2, D2 = _engine.fused_fwd_d(xg, yg, 0.7, bw)
+    assert torch.equal(D1, D2) and torch.equal(R1, R2) and torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("bandwidth", [None, 15.0])
+def test_unfused_module_matches_two_node_graph(bandwidth):
+    # SoftDTW(fused=False) takes the one-launch forward; its loss and gradients equal those of
+    # pairwise_distance followed by SoftDTWAutograd (the reference's unfused graph)
+    from softdtw_cuda import SoftDTW
+    from softdtw_cuda.autograd import SoftDTWAutograd
+    from softdtw_cuda.distances import pairwise_distance
+
+    x, y = randn_pair(4, 90, 70, 8, seed=3)
+    xa, ya = x.cuda().requires_grad_(True), y.cuda().requires_grad_(True)
+    out_a = SoftDTW(gamma=0.5, bandwidth=bandwidth, fused=False)(xa, ya)
+    out_a.sum().backward()
+    xb, yb = x.cuda().requires_grad_(True), y.cuda().requires_grad_(True)
+    out_b = SoftDTWAutograd.apply(pairwise_distance(xb, yb, dist="sqeuclidean"), 0.5, bandwidth)
+    out_b.sum().backward()
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(xa.grad, xb.grad) and torch.equal(ya.grad, yb.grad)
