@@ -409,10 +409,12 @@ def main(argv=None):
 
     # per-kernel timing (HIP events on the engine's stream) -> dominant kernel roofline
     kernels = []
-    # unfused mode's forward: one launch forming D and R (fused_fwd_d), except under "fast"
-    # arithmetic, where the module keeps the distance and the recursion apart
-    unfused_kernels = (["dist_fwd", "dp_fwd", "dp_bwd", "dist_bwd"] if args.numerics == "fast"
-                       else ["fused_fwd_d", "dp_bwd", "dist_bwd"])
+    # unfused mode's forward: one launch forming D and R (fused_fwd_d) where the module takes
+    # it (not under "fast" arithmetic), else the distance and the recursion apart
+    from softdtw_cuda import _engine
+    unfused_kernels = (["fused_fwd_d", "dp_bwd", "dist_bwd"]
+                       if _engine.one_launch_unfused_forward(B, N, M, K, X.device)
+                       else ["dist_fwd", "dp_fwd", "dp_bwd", "dist_bwd"])
     if "unfused" in res:
         kernels += unfused_kernels
     if "fused" in res:

@@ -8,6 +8,7 @@ missing or no GPU is present, they raise.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 
@@ -311,6 +312,26 @@ def fused_costs_on_matrix_cores(N: int, M: int, K: int) -> bool:
     (K <= 64 and K*N*M >= 400: the shapes whose reference dot is a fused multiply-add
     chain), which sdtw_fused_fwd_d_f32 needs."""
     return K <= 64 and K * N * M >= 400
+
+
+@functools.lru_cache(maxsize=None)
+def _cu_count(index: int) -> int:
+    return torch.cuda.get_device_properties(index).multi_processor_count
+
+
+def one_launch_unfused_forward(B: int, N: int, M: int, K: int, device) -> bool:
+    """Whether sdtw_fused_fwd_d_f32 beats the distance launch plus the D-reading recursion.
+    It needs matrix-core costs, and the batch's 2-band workgroups must all fit on the GPU at
+    once (B * ceil(ceil(N/64)/2) <= CU count, the library's own choice): the producer waves
+    then have SIMDs of their own, whereas sharing their compute waves' SIMDs, the D stores
+    slow the recursion (B=32 N=M=2048 D=64: 2.78 against 2.70 ms per step).  Not under
+    "fast" arithmetic, whose short recursion step makes the storing producers the limit."""
+    if not fused_costs_on_matrix_cores(N, M, K) or get_numerics() == "fast":
+        return False
+    bands = -(-N // 64)
+    groups = -(-bands // 2)  # workgroups per pair at 2 bands each
+    index = torch.device(device).index
+    return B * groups <= _cu_count(torch.cuda.current_device() if index is None else index)
 
 
 def fused_fwd_d(x, y, gamma: float, bandwidth: float):

@@ -117,16 +117,14 @@ class SoftDTW(nn.Module):
 
 
 def _unfused(x, y, gamma, bandwidth, dist):
-    """pairwise_distance, then SoftDTWAutograd over the cost.  For float32 GPU inputs whose
-    costs come from the matrix cores, both forwards run in one launch
-    (SoftDTWSqEuclidAutograd), with the same results.  Not under "fast" arithmetic: there
-    the recursion outpaces the producer waves once they also store D, and two launches are
-    quicker (0.165 ms against 0.173 ms at B=32 N=M=512 D=64)."""
+    """pairwise_distance, then SoftDTWAutograd over the cost.  For float32 GPU inputs of the
+    shapes where it is quicker (_engine.one_launch_unfused_forward), both forwards run in one
+    launch (SoftDTWSqEuclidAutograd), with the same results."""
     if (x.dtype == torch.float32 and y.dtype == torch.float32 and x.is_cuda and y.is_cuda
             and x.device == y.device
             and dist.lower() in _SQEUCLID_NAMES
-            and _engine.get_numerics() != "fast"
-            and _engine.fused_costs_on_matrix_cores(x.shape[1], y.shape[1], x.shape[2])):
+            and _engine.one_launch_unfused_forward(x.shape[0], x.shape[1], y.shape[1],
+                                                   x.shape[2], x.device)):
         return SoftDTWSqEuclidAutograd.apply(x.contiguous(), y.contiguous(), gamma, bandwidth)
     D = pairwise_distance(x, y, dist=dist)
     return SoftDTWAutograd.apply(D, gamma, bandwidth)
