@@ -17,6 +17,7 @@ of the reference's CPU path (oracle/) on the host cores.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -108,6 +109,22 @@ def kernel_launcher(name, xg, yg, gamma):
     return fn
 
 
+class _no_gc:
+    """Collect garbage before a timed region and keep the collector off inside it, as
+    timeit does: a full collection of the interpreter's objects (tens of ms with torch
+    loaded) otherwise lands, at an allocation-count-determined point, inside a host-bound
+    step of a few hundred microseconds."""
+
+    def __enter__(self):
+        self.was = gc.isenabled()
+        gc.collect()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        if self.was:
+            gc.enable()
+
+
 def time_kernel(fn, launches, warmup=2):
     import torch
 
@@ -117,11 +134,12 @@ def time_kernel(fn, launches, warmup=2):
     st = torch.cuda.current_stream()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(launches)]
-    for a, b in evs:
-        a.record(st)
-        fn()
-        b.record(st)
-    torch.cuda.synchronize()
+    with _no_gc():
+        for a, b in evs:
+            a.record(st)
+            fn()
+            b.record(st)
+        torch.cuda.synchronize()
     return statistics.mean(a.elapsed_time(b) for a, b in evs)
 
 
@@ -135,12 +153,13 @@ def time_steps(step, steps, warmup):
     st = torch.cuda.current_stream()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    a.record(st)
-    for _ in range(steps):
-        step()
-    b.record(st)
-    torch.cuda.synchronize()
+    with _no_gc():
+        torch.cuda.synchronize()
+        a.record(st)
+        for _ in range(steps):
+            step()
+        b.record(st)
+        torch.cuda.synchronize()
     ms = a.elapsed_time(b) / steps
     peak = torch.cuda.max_memory_allocated() / 2 ** 20
     return ms, peak
