@@ -58,3 +58,26 @@ def test_workspace_sizes():
     assert lib.sdtw_workspace_bytes(_engine.OP_FWD, B, N, M, K) >= 8 * B * M
     assert lib.sdtw_workspace_bytes(_engine.OP_FUSED_BWD, B, N, M, K) >= 4 * B * N * M
     assert lib.sdtw_workspace_bytes(99, B, N, M, K) == 0
+
+
+def test_one_launch_unfused_forward_choice(monkeypatch):
+    # the unfused module takes the one-launch forward only with matrix-core costs, in the
+    # 2-band geometry (B * ceil(ceil(N/64)/2) <= CU count) and outside "fast" arithmetic
+    monkeypatch.setattr(_engine, "_cu_count", lambda index: 256)
+    prev = _engine.set_numerics("mixed")
+    try:
+        pick = _engine.one_launch_unfused_forward
+        assert pick(32, 512, 512, 64, "cuda:0")         # 32 * 4 = 128 workgroups
+        assert pick(32, 1024, 1024, 64, "cuda:0")       # 32 * 8 = 256: still fits
+        assert not pick(32, 2048, 2048, 64, "cuda:0")   # 32 * 16 = 512: 4-band geometry
+        assert pick(256, 64, 64, 8, "cuda:0")           # one band per pair
+        assert not pick(257, 64, 64, 8, "cuda:0")
+        assert pick(16, 2048, 2048, 1, "cuda:0")
+        assert not pick(4, 512, 512, 65, "cuda:0")      # K > 64: scalar cost tiles
+        assert not pick(1, 5, 5, 3, "cuda:0")           # K*N*M < 400: scalar cost tiles
+        assert _engine.set_numerics("exact") == "mixed"
+        assert pick(32, 512, 512, 64, "cuda:0")
+        _engine.set_numerics("fast")
+        assert not pick(32, 512, 512, 64, "cuda:0")
+    finally:
+        _engine.set_numerics(prev)
