@@ -345,13 +345,14 @@ static int fused_fwd_common(const float* x, const float* y, float* D, float* R, 
     const int wmax = fused_wmax(B, N, M, K);
     const DPScratch d = carve_dp(c, B, N, M, wmax);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
-    if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess) return SDTW_ERR_LAUNCH;
     DPParams p{};
     fill_dp(p, d, B, N, M, K, gamma, bandwidth, wmax);
     p.x = x;
     p.y = y;
     p.x2 = x2;
     p.y2 = y2;
+    p.x2_fill = x2;  // the norms are formed by the prep launch
+    p.y2_fill = y2;
     p.R = R;
     p.out = out;
     p.D_out = D;
@@ -374,18 +375,20 @@ int sdtw_fused_fwd_d_f32(const float* x, const float* y, float* D, float* R, flo
     return fused_fwd_common(x, y, D, R, out, B, N, M, K, gamma, bandwidth, ws, ws_bytes, stream);
 }
 
-// Fused backward core: norms, then the reverse wavefront writing gout * E into `E`.
+// Fused backward core: norms (formed by the prep launch), then the reverse wavefront writing
+// gout * E into `E`.
 static int fused_bwd_common(const float* x, const float* y, const float* R, const float* gout,
                             float* E, float* x2, float* y2, const DPScratch& d, int64_t B,
                             int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
                             hipStream_t st) {
-    if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess) return SDTW_ERR_LAUNCH;
     DPParams p{};
     fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_wmax(B, N, M, K));
     p.x = x;
     p.y = y;
     p.x2 = x2;
     p.y2 = y2;
+    p.x2_fill = x2;
+    p.y2_fill = y2;
     p.R = const_cast<float*>(R);
     p.gout = gout;
     p.G_out = E;

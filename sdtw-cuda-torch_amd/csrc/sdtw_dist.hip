@@ -44,14 +44,11 @@ SDTW_DEV float row_norm8(const float* row, int K, int t, bool ok) {
     return (ok && t == 0) ? __fadd_rn(0.0f, aten_row_sum_sq(row, 1, K)) : 0.0f;
 }
 
-// Norms of two row sets in one launch: rows [0, rows0) of v0 into out0, then rows0 more
-// of v1 into out1.
-__global__ void __launch_bounds__(256) norms_kernel(const float* __restrict__ v0,
-                                                    float* __restrict__ out0, int64_t rows0,
-                                                    const float* __restrict__ v1,
-                                                    float* __restrict__ out1, int64_t rows1,
-                                                    int K) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Norms of two row sets, eight threads per row, thread gid of the grid: rows [0, rows0) of
+// v0 into out0, then rows1 more of v1 into out1.
+SDTW_DEV void norms_at(int64_t gid, const float* __restrict__ v0, float* __restrict__ out0,
+                       int64_t rows0, const float* __restrict__ v1, float* __restrict__ out1,
+                       int64_t rows1, int K) {
     const int64_t r = gid >> 3;
     const int t = (int)(gid & 7);
     const bool first = r < rows0;
@@ -60,6 +57,44 @@ __global__ void __launch_bounds__(256) norms_kernel(const float* __restrict__ v0
     const float* row = (first ? v0 : v1) + (ok ? rr : 0) * K;
     const float v = row_norm8(row, K, t, ok);
     if (ok && t == 0) (first ? out0 : out1)[rr] = v;
+}
+
+__global__ void __launch_bounds__(256) norms_kernel(const float* __restrict__ v0,
+                                                    float* __restrict__ out0, int64_t rows0,
+                                                    const float* __restrict__ v1,
+                                                    float* __restrict__ out1, int64_t rows1,
+                                                    int K) {
+    norms_at((int64_t)blockIdx.x * blockDim.x + threadIdx.x, v0, out0, rows0, v1, out1, rows1, K);
+}
+
+// Blocks [0, prep_blocks) do the wavefront launch's prep work, the rest the norms (each block
+// takes one job whole, so the norms' shuffles stay within full waves).
+__global__ void __launch_bounds__(256) prep_norms_kernel(
+    int* ticket, int* err, unsigned long long* rows, int64_t nwords, unsigned long long lo,
+    unsigned long long hi, int prep_blocks, const float* __restrict__ v0,
+    float* __restrict__ out0, int64_t rows0, const float* __restrict__ v1,
+    float* __restrict__ out1, int64_t rows1, int K) {
+    const int b = (int)blockIdx.x;
+    if (b < prep_blocks) {
+        prep_rows((int64_t)b * blockDim.x + threadIdx.x, (int64_t)prep_blocks * blockDim.x,
+                  ticket, err, rows, nwords, lo, hi);
+        return;
+    }
+    norms_at((int64_t)(b - prep_blocks) * blockDim.x + threadIdx.x, v0, out0, rows0, v1, out1,
+             rows1, K);
+}
+
+hipError_t launch_prep_norms(int* ticket, int* err, unsigned long long* rows, int64_t nwords,
+                             unsigned long long lo, unsigned long long hi, const float* x,
+                             float* x2, int64_t rows_x, const float* y, float* y2,
+                             int64_t rows_y, int K, hipStream_t st) {
+    int64_t prep = (nwords + 255) / 256;
+    prep = prep < 1 ? 1 : (prep > 1024 ? 1024 : prep);
+    const int64_t norm_blocks = ((rows_x + rows_y) * 8 + 255) / 256;
+    hipLaunchKernelGGL(prep_norms_kernel, dim3((unsigned)(prep + norm_blocks)), dim3(256), 0, st,
+                       ticket, err, rows, nwords, lo, hi, (int)prep, x, x2, rows_x, y, y2, rows_y,
+                       K);
+    return hipGetLastError();
 }
 
 hipError_t launch_norms(const float* x, float* x2, int64_t rows_x, const float* y, float* y2,

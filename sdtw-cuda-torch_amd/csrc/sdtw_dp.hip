@@ -8,14 +8,8 @@ namespace sdtw {
 // Zero the ticket and error flag; mark every entry of the cross-workgroup rows empty.
 __global__ void prep_kernel(int* ticket, int* err, unsigned long long* rows, int64_t nwords,
                             unsigned long long lo, unsigned long long hi) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx == 0) {
-        *ticket = 0;
-        *err = 0;
-    }
-    // forward rows: one 64-bit word per entry (lo == hi); backward rows: two words (E,R)
-    // and (D,tag) per entry
-    for (int64_t k = idx; k < nwords; k += (int64_t)gridDim.x * blockDim.x) rows[k] = (k & 1) ? hi : lo;
+    prep_rows((int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x,
+              ticket, err, rows, nwords, lo, hi);
 }
 
 hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st) {
@@ -23,6 +17,10 @@ hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st) {
     const int64_t nwords = bwd ? 2 * entries : entries;
     const unsigned long long lo = bwd ? (unsigned long long)kEmpty32 : kEmpty64;
     const unsigned long long hi = bwd ? 0ull : kEmpty64;
+    if (P.x2_fill)  // with the fused recursions' row norms
+        return launch_prep_norms(P.ticket, P.err, reinterpret_cast<unsigned long long*>(P.gring),
+                                 nwords, lo, hi, P.x, P.x2_fill, (int64_t)P.B * P.N, P.y,
+                                 P.y2_fill, (int64_t)P.B * P.M, P.K, st);
     int64_t blocks = (nwords + 255) / 256;
     blocks = blocks < 1 ? 1 : (blocks > 2048 ? 2048 : blocks);
     hipLaunchKernelGGL(prep_kernel, dim3((unsigned)blocks), dim3(256), 0, st, P.ticket, P.err,

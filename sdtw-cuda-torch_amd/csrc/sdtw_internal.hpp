@@ -18,6 +18,8 @@ struct DPParams {
     float* G_out;       // backward: (B,N,M) = gout * E
     const float* gout;  // backward: (B) upstream gradient or nullptr (= 1)
     float* D_out;       // fused forward: the cost tiles also stored here (B,N,M), or nullptr
+    float* x2_fill;     // fused: x2 / y2 (writable) for the prep launch to form, or nullptr
+    float* y2_fill;
     int* ticket;        // workgroup ticket counter (zeroed by the prep kernel)
     double* gring;      // forward: (B*G, RW) fp64 last rows of each workgroup's bands
     float4* gring4;     // backward: (B*G, RW) (E, R, D, tag) first rows
@@ -86,6 +88,25 @@ inline int64_t dist_bwd_flags(int64_t B, int64_t N, int64_t M, int64_t K) {
     return dist_bwd_tiles(B, N, K) * dist_bwd_splits(B, N, M, K);
 }
 
+// The prep work of one thread of a grid of `stride` threads: thread 0 zeroes the workgroup
+// ticket and the error flag; every thread marks its share of the cross-workgroup rows empty
+// (forward rows: one 64-bit word per entry, lo == hi; backward rows: the words (E,R) and
+// (D,tag) of each entry, lo and hi).
+__device__ inline void prep_rows(int64_t idx, int64_t stride, int* ticket, int* err,
+                                 unsigned long long* rows, int64_t nwords,
+                                 unsigned long long lo, unsigned long long hi) {
+    if (idx == 0) {
+        *ticket = 0;
+        *err = 0;
+    }
+    for (int64_t k = idx; k < nwords; k += stride) rows[k] = (k & 1) ? hi : lo;
+}
+// The prep work and the row norms of x and y in one launch (the fused recursions need both
+// before they start).
+hipError_t launch_prep_norms(int* ticket, int* err, unsigned long long* rows, int64_t nwords,
+                             unsigned long long lo, unsigned long long hi, const float* x,
+                             float* x2, int64_t rows_x, const float* y, float* y2,
+                             int64_t rows_y, int K, hipStream_t st);
 hipError_t launch_norms(const float* x, float* x2, int64_t rows_x, const float* y, float* y2,
                         int64_t rows_y, int K, hipStream_t st);
 hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t st);
