@@ -219,3 +219,26 @@ def test_unfused_module_matches_two_node_graph(bandwidth):
     out_b.sum().backward()
     assert torch.equal(out_a, out_b)
     assert torch.equal(xa.grad, xb.grad) and torch.equal(ya.grad, yb.grad)
+
+
+def test_unfused_normalize_matches_two_node_graph():
+    # normalize=True, fused=False: x-y minus half of x-x and y-y, each term through the
+    # one-launch forward; equal to pairwise_distance + SoftDTWAutograd term by term
+    from softdtw_cuda import SoftDTW
+    from softdtw_cuda.autograd import SoftDTWAutograd
+    from softdtw_cuda.distances import pairwise_distance
+
+    x, y = randn_pair(3, 80, 80, 8, seed=11)
+    xa, ya = x.cuda().requires_grad_(True), y.cuda().requires_grad_(True)
+    out_a = SoftDTW(gamma=0.5, normalize=True, fused=False)(xa, ya)
+    out_a.sum().backward()
+    xb, yb = x.cuda().requires_grad_(True), y.cuda().requires_grad_(True)
+
+    def term(a, b):
+        return SoftDTWAutograd.apply(pairwise_distance(a, b, dist="sqeuclidean"), 0.5, None)
+
+    out_b = term(xb, yb) - 0.5 * (term(xb, xb) + term(yb, yb))
+    out_b.sum().backward()
+    torch.testing.assert_close(out_a, out_b, rtol=1e-6, atol=1e-5)
+    torch.testing.assert_close(xa.grad, xb.grad, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(ya.grad, yb.grad, rtol=1e-5, atol=1e-6)
