@@ -53,15 +53,15 @@ typedef enum sdtw_op {
     SDTW_OP_FUSED_BWD = 5
 } sdtw_op;
 
-/* Distance modes for sdtw_sqeuclid_fwd_f32. */
+/* Distance modes for sdtw_sqeuclid_fwd_f32 (one mode). */
 typedef enum sdtw_dist_mode {
     /* Same fp32 bits as the reference's torch-CPU distance (distances.py:20-28) on an x86
      * host: row norms in ATen's 8-lane cascade order, x.y^T as a sequential FMA chain over
-     * k (plain multiply-then-add when K*N*M < 400, ATen's small-matrix kernel). */
-    SDTW_DIST_EXACT = 0,
-    /* x.y^T on the matrix cores (v_mfma_f32_16x16x4_f32); norms as in EXACT.  Faster, but
-     * the k-sum is reassociated, so D differs from the reference by a few ulp. */
-    SDTW_DIST_MFMA = 1
+     * k (plain multiply-then-add when K*N*M < 400, ATen's small-matrix kernel).  For
+     * K <= 64 the chain runs on the matrix cores: v_mfma_f32_16x16x4_f32 chained over k from
+     * a zero accumulator gives the sequential chain's bits, so no faster inexact mode is
+     * offered. */
+    SDTW_DIST_EXACT = 0
 } sdtw_dist_mode;
 
 /* Cell arithmetic of the Soft-DTW recursions (sdtw_set_numerics). */
@@ -95,10 +95,27 @@ int sdtw_get_numerics(void);
 
 /* Diagnostic (synchronises the device): SDTW_ERR_TIMEOUT if the last wavefront launch of
  * `op` that used workspace `ws` hit its bounded inter-band wait, else SDTW_OK.  The kernels
- * never hang: a wait that expires raises this flag and the wave exits.  No counterpart in
- * the reference (whose kernels have no inter-block waits). */
+ * never hang: a wait that expires raises this flag, the wave stops, and the pair's results
+ * are marked invalid without any synchronisation -- out[p] = NaN (forward), NaN over the
+ * band's rows of G or E (backward), and so NaN gradients through the distance backward.
+ * No counterpart in the reference (whose kernels have no inter-block waits). */
 int sdtw_debug_status(int op, const void *ws, size_t ws_bytes, int64_t B, int64_t N, int64_t M,
                       int64_t K);
+
+/* Polls a wavefront kernel's bounded wait makes before it gives up, for every later launch in
+ * this process; returns the previous value.  The default, 2^22, is about 0.3 s without
+ * progress.  A test hook: a tiny limit makes the waits that would have to poll give up at
+ * once (every kernel still exits normally), so the give-up path can be exercised.  No
+ * counterpart in the reference. */
+unsigned sdtw_set_wait_limit(unsigned polls);
+
+/* Bands per workgroup the fused recursions (sdtw_fused_fwd_f32, sdtw_fused_fwd_d_f32,
+ * sdtw_fused_bwd_f32) take at this shape on the current device: 2 when the batch's 2-band
+ * workgroups all fit on the GPU at once (their matrix-core producer waves then have SIMDs of
+ * their own), else 4; 0 for an invalid shape.  The choice the launcher makes, exported so a
+ * caller can choose between sdtw_fused_fwd_d_f32 and the two-call unfused forward.  No
+ * counterpart in the reference. */
+int sdtw_fused_bands_per_workgroup(int64_t B, int64_t N, int64_t M, int64_t K);
 
 /* Number of floats of the R table for B pairs of N x M cells. */
 int64_t sdtw_table_elems(int64_t B, int64_t N, int64_t M);

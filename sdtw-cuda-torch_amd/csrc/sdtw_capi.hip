@@ -120,6 +120,9 @@ DPScratch carve_dp(Carver& c, int64_t B, int64_t N, int64_t M, int wmax = 4) {
     return d;
 }
 
+// Process-wide poll limit of the wavefront kernels' bounded waits (sdtw_set_wait_limit).
+std::atomic<unsigned> g_spin_limit{kDefaultSpinLimit};
+
 void fill_dp(DPParams& p, const DPScratch& d, int64_t B, int64_t N, int64_t M, int64_t K,
              double gamma, double bandwidth, int wmax = 4) {
     const DPGeom g = dp_geom(N, wmax);
@@ -139,6 +142,7 @@ void fill_dp(DPParams& p, const DPScratch& d, int64_t B, int64_t N, int64_t M, i
     p.gamma = gamma;
     p.inv_gamma = 1.0 / gamma;
     p.bw = bandwidth;
+    p.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
 }
 
 int status_of(hipError_t e) { return e == hipSuccess ? SDTW_OK : SDTW_ERR_LAUNCH; }
@@ -165,7 +169,7 @@ const char* sdtw_strerror(int status) {
     }
 }
 
-int sdtw_version(void) { return 4; }
+int sdtw_version(void) { return 5; }
 
 int sdtw_set_numerics(int mode) {
     if (mode != SDTW_NUMERICS_FAST && mode != SDTW_NUMERICS_EXACT && mode != SDTW_NUMERICS_MIXED)
@@ -174,6 +178,13 @@ int sdtw_set_numerics(int mode) {
 }
 
 int sdtw_get_numerics(void) { return g_numerics.load(); }
+
+unsigned sdtw_set_wait_limit(unsigned polls) { return g_spin_limit.exchange(polls); }
+
+int sdtw_fused_bands_per_workgroup(int64_t B, int64_t N, int64_t M, int64_t K) {
+    if (!shape_ok(B, N, M, K, true)) return 0;
+    return fused_wmax(B, N, M, K);
+}
 
 int sdtw_debug_status(int op, const void* ws, size_t ws_bytes, int64_t B, int64_t N, int64_t M,
                       int64_t K) {

@@ -45,7 +45,6 @@ namespace sdtw {
 constexpr int WAVE = 64;
 constexpr int U = 16;     // steps per group (the unit of prefetch and of band handover)
 constexpr int RS = 128;   // LDS ring slots per band boundary (power of two, multiple of U)
-constexpr unsigned kSpinLimit = 1u << 22;
 constexpr int RPAD = 64;  // padding entries on each side of a cross-workgroup row
 
 // ---------------------------------------------------------------------------------------
@@ -116,19 +115,22 @@ SDTW_DEV float4 glb_get_entry(const float4* p) { return glb_get4(p); }
 SDTW_DEV bool entry_empty(double v) { return row_empty(v); }
 SDTW_DEV bool entry_empty(float4 v) { return row_empty4(v); }
 
-// Spin until the LDS counter *flag >= need.  Returns false (and raises the error flag) on
-// timeout.  `known` caches the last value read; every lane reads the same counter, so it is
-// kept wave-uniform (a scalar register) and the loop branches on scalar compares.
-SDTW_DEV bool wait_at_least(const int* flag, int need, int& known, int* err) {
+SDTW_DEV void raise_timeout(int* err) { __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Spin until the LDS counter *flag >= need.  Returns false (and raises the error flag) after
+// `limit` polls that found it short.  `known` caches the last value read; every lane reads
+// the same counter, so it is kept wave-uniform (a scalar register) and the loop branches on
+// scalar compares.
+SDTW_DEV bool wait_at_least(const int* flag, int need, int& known, int* err, unsigned limit) {
     unsigned spins = 0;
     while (known < need) {
         known = __builtin_amdgcn_readfirstlane(lds_load(flag));
         if (known >= need) break;
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins > kSpinLimit) {
-            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (spins++ >= limit) {
+            raise_timeout(err);
             return false;
         }
+        __builtin_amdgcn_s_sleep(1);
     }
     // the ring accesses the wait guards must not be moved above the counter read; the
     // hardware performs a wave's LDS operations in order, so a compiler fence suffices
@@ -136,7 +138,30 @@ SDTW_DEV bool wait_at_least(const int* flag, int need, int& known, int* err) {
     return true;
 }
 
-SDTW_DEV void raise_timeout(int* err) { __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// A wave whose bounded wait expired stops, and marks its pair's results invalid where a
+// caller reads them without a synchronisation: the forward sets out[p] to NaN, the backward
+// fills its band's rows of G with NaN.  Every wave that depends on the stopped one (bands
+// further along the pair, the band's own compute or producer wave) then also gives up, since
+// the entries it waits for never arrive; so the last band of the pair never stores a value
+// over the NaN.  The flag (sdtw_debug_status) is raised too.
+SDTW_DEV void give_up_fwd(const DPParams& P, int p) {
+    raise_timeout(P.err);
+    if ((threadIdx.x & 63) == 0) P.out[p] = __builtin_nanf("");
+}
+SDTW_DEV void give_up_bwd(const DPParams& P, int p, int b) {
+    raise_timeout(P.err);
+    const int r0 = b * 64;
+    const int nrows = min(P.N - r0, 64);
+    if (nrows <= 0) return;
+    float* base = P.G_out + ((int64_t)p * P.N + r0) * P.M;
+    const int64_t cells = (int64_t)nrows * P.M;
+    for (int64_t e = threadIdx.x & 63; e < cells; e += 64) base[e] = __builtin_nanf("");
+}
+template <bool BWD>
+SDTW_DEV void give_up(const DPParams& P, int p, int b) {
+    if constexpr (BWD) give_up_bwd(P, p, b);
+    else give_up_fwd(P, p);
+}
 
 // Slot of entry c (a column, or a backward sequence number) in an LDS handoff ring.  The
 // rotation by 63 puts the U entries a band hands over per group (c = s0 - 63 .. s0 - 48, for
@@ -267,13 +292,14 @@ struct CostD {
 #pragma unroll
         for (int k = 0; k < 16; ++k) dst[4 * k * CS] = v[k];
     }
-    SDTW_DEV void prologue(float* ring, int c) {
+    SDTW_DEV bool prologue(float* ring, int c) {
         issue(c);
         store(ring, c);
+        return true;
     }
     SDTW_DEV void preload(int) {}
     // the tile is loaded at the first step and lands in the ring after the last one
-    SDTW_DEV void begin(float*, int) {}
+    SDTW_DEV bool begin(float*, int) { return true; }
     SDTW_DEV void step(int u, int c, int) {
         if (u == 0) {
             issue(c);
@@ -347,17 +373,21 @@ struct CostMfma {
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) acc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    SDTW_DEV void prologue(float* ring, int c) {
+    SDTW_DEV bool prologue(float* ring, int c) {
         issue(c);
         zero();
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) mma(kk);
         finish(ring, c);
+        return true;
     }
     SDTW_DEV void preload(int c) { issue(c); }
     // one k-step per recursion step, so the matrix pipe never holds up the wave's in-order
     // issue; the next tile's B operand is loaded after the last product has read it
-    SDTW_DEV void begin(float*, int) { zero(); }
+    SDTW_DEV bool begin(float*, int) {
+        zero();
+        return true;
+    }
     SDTW_DEV void step(int u, int, int) {
         if (u < NKK) mma(u);
     }
@@ -414,9 +444,12 @@ struct CostScalar {
         x2 = P.x2 + (int64_t)p * N;
         y2 = P.y2 + (int64_t)p * M;
     }
-    SDTW_DEV void prologue(float* ring, int c) { finish(ring, c); }
+    SDTW_DEV bool prologue(float* ring, int c) {
+        finish(ring, c);
+        return true;
+    }
     SDTW_DEV void preload(int) {}
-    SDTW_DEV void begin(float*, int) {}
+    SDTW_DEV bool begin(float*, int) { return true; }
     SDTW_DEV void step(int, int, int) {}
     SDTW_DEV void end(float* ring, int c, int) { finish(ring, c); }
     SDTW_DEV void finish(float* ring, int c0) {
@@ -464,16 +497,16 @@ struct CostRing {
     const int* ready;
     int* done;
     int* err;
+    unsigned limit;
     int known, groups, pro;
-    SDTW_DEV void bind(const Smem& sm, int w, int* e);
+    SDTW_DEV void bind(const Smem& sm, int w, const DPParams& P);
     SDTW_DEV void init(const DPParams&, int, int) {}
-    SDTW_DEV void wait(int n) {
-        if (!wait_at_least(ready, n, known, err)) known = 1 << 30;  // timed out: flag raised
-    }
+    // false: the wait expired (flag raised); the compute wave then stops
+    SDTW_DEV bool wait(int n) { return wait_at_least(ready, n, known, err, limit); }
     // the two prologue tiles
-    SDTW_DEV void prologue(float*, int) { wait(++pro); }
+    SDTW_DEV bool prologue(float*, int) { return wait(++pro); }
     SDTW_DEV void preload(int) {}
-    SDTW_DEV void begin(float*, int) { wait(groups + 2); }
+    SDTW_DEV bool begin(float*, int) { return wait(groups + 2); }
     SDTW_DEV void step(int, int, int) {}
     SDTW_DEV void end(float*, int, int) {
         ++groups;
@@ -513,10 +546,11 @@ struct Smem {
     }
 };
 
-SDTW_DEV void CostRing::bind(const Smem& sm, int w, int* e) {
+SDTW_DEV void CostRing::bind(const Smem& sm, int w, const DPParams& P) {
     ready = sm.ready() + w;
     done = sm.done() + w;
-    err = e;
+    err = P.err;
+    limit = P.spin_limit;
     known = 0;
     groups = 0;
     pro = 0;
@@ -588,7 +622,10 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
             for (int kk = 0; kk < Src::NKK; ++kk) c.mma(kk);
         }
         const int need = BWD ? t - 3 : t - 4;
-        if (need > 0 && !wait_at_least(done, need, known, P.err)) return;
+        if (need > 0 && !wait_at_least(done, need, known, P.err, P.spin_limit)) {
+            give_up<BWD>(P, p, b);
+            return;
+        }
         GTile gt;
         const bool flush = BWD && t >= 4;
         if (flush) gt.read(P, ring, (t - 4) * U);
@@ -605,7 +642,10 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
     }
     if (BWD) {
         for (int g = max(T - 4, 0); g < groups; ++g) {
-            if (!wait_at_least(done, g + 1, known, P.err)) return;
+            if (!wait_at_least(done, g + 1, known, P.err, P.spin_limit)) {
+                give_up<BWD>(P, p, b);
+                return;
+            }
             GTile gt;
             gt.read(P, ring, g * U);
             gt.write(P, p, b);
@@ -668,7 +708,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     auto fetch_lds = [&](int c0, double* dst) -> bool {
         const bool live = b > 0 && c0 < M;
         const int need = min(c0 + U, M);
-        if (live && !wait_at_least(lin_flag, need, known_in, P.err)) return false;
+        if (live && !wait_at_least(lin_flag, need, known_in, P.err, P.spin_limit)) return false;
         const double* blk = lin + hslot(c0 + 1);  // entries c0 + 1 .. c0 + U - 1
         dst[0] = lin[hslot(c0)];
         const double2* src = reinterpret_cast<const double2*>(blk);
@@ -706,8 +746,10 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     //   - the band above's row is read from the LDS ring at the group start (reading it
     //     a group ahead would add a group of lag per band boundary).
     // Tiles past the table are harmless: loads are clamped and their slots are not live.
-    cost.prologue(cring, 0);
-    cost.prologue(cring, TC);
+    if (!cost.prologue(cring, 0) || !cost.prologue(cring, TC)) {
+        give_up_fwd(P, p);
+        return;
+    }
     cost.preload(2 * TC);
 #pragma unroll
     for (int u = 0; u < U; ++u) d_nxt[u] = crow[(u - l) & (CR - 1)];
@@ -715,13 +757,18 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     for (int s0 = 0; s0 < S; s0 += U) {
 #pragma unroll
         for (int u = 0; u < U; ++u) d_cur[u] = d_nxt[u];
-        cost.begin(cring, s0 + 2 * TC);
-        if (!fetch_lds(s0, up_cur)) return;
+        if (!cost.begin(cring, s0 + 2 * TC) || !fetch_lds(s0, up_cur)) {
+            give_up_fwd(P, p);
+            return;
+        }
         // this group writes columns up to s0 + U - 64 of my last row; writing column c
         // reuses the slot of column c - RS, which the consumer must have taken
         if (out_lds) {
             const int need_free = s0 + U - WAVE + 1 - RS;
-            if (need_free > 0 && !wait_at_least(sm.cons() + (w + 1), need_free, known_free, P.err)) return;
+            if (need_free > 0 && !wait_at_least(sm.cons() + (w + 1), need_free, known_free, P.err, P.spin_limit)) {
+                give_up_fwd(P, p);
+                return;
+            }
         }
         float* Rg = Rt + (int64_t)s0 * WAVE;
 #pragma unroll
@@ -772,7 +819,7 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
     unsigned spins = 0;
     for (int c = 0; c < M;) {
         const int need_free = c + WAVE - RS;
-        if (need_free > 0 && !wait_at_least(sm.cons() + k, need_free, known_free, P.err)) return;
+        if (need_free > 0 && !wait_at_least(sm.cons() + k, need_free, known_free, P.err, P.spin_limit)) return;
         const int e = c + l;
         T v;
         bool empty = false;
@@ -788,11 +835,11 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
             if (l == 0) lds_publish(sm.prod() + k, c);
             spins = 0;
         } else {
-            __builtin_amdgcn_s_sleep(2);
-            if (++spins > kSpinLimit) {
-                raise_timeout(P.err);
+            if (spins++ >= P.spin_limit) {
+                raise_timeout(P.err);  // the compute wave it feeds then gives up
                 return;
             }
+            __builtin_amdgcn_s_sleep(2);
         }
     }
 }
@@ -834,7 +881,7 @@ __global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPPara
             producer_wave<Cost, false>(P, sm, p, g * P.W + wb, wb);
         } else {
             CostRing cost;
-            cost.bind(sm, w, P.err);
+            cost.bind(sm, w, P);
             fwd_band<CostRing, BAND, EXACT>(P, cost, sm, p, g, w);
         }
     } else {
@@ -914,7 +961,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         for (int u = 0; u < U; ++u) dst[u] = make_float4(0.0f, NINF, 0.0f, 1.0f);
         if (b + 1 >= nb || q0 >= M) return true;
         const int need = min(q0 + U, M);
-        if (!wait_at_least(lin_flag, need, known_in, P.err)) return false;
+        if (!wait_at_least(lin_flag, need, known_in, P.err, P.spin_limit)) return false;
 #pragma unroll
         for (int u = 0; u < U; ++u) dst[u] = u == 0 ? lin[hslot(q0)] : lin[hslot(q0 + 1) + u - 1];
         if (l == 0) lds_publish(sm.cons() + (w + 1), need);
@@ -956,8 +1003,10 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // pipeline is the forward's, mirrored
     auto tile_col = [&](int q0) { return M - TC - q0; };
     auto ring_col = [&](int q) { return ((M - 1) - q + (WAVE - 1 - l)) & (CR - 1); };
-    cost.prologue(cring, tile_col(0));
-    cost.prologue(cring, tile_col(TC));
+    if (!cost.prologue(cring, tile_col(0)) || !cost.prologue(cring, tile_col(TC))) {
+        give_up_bwd(P, p, b);
+        return;
+    }
     cost.preload(tile_col(2 * TC));
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -981,12 +1030,11 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             r_cur[u] = r_nxt[u];
             d_cur[u] = d_nxt[u];
         }
-        cost.begin(cring, tile_col(q0 + 2 * TC));
-        if (!fetch_lds(q0, dn_cur)) return false;
+        if (!cost.begin(cring, tile_col(q0 + 2 * TC)) || !fetch_lds(q0, dn_cur)) return false;
         const int n0 = q0 + U;
         if (out_lds) {  // as in the forward: sequence numbers up to q0 + U - 64 this group
             const int need_free = q0 + U - WAVE + 1 - RS;
-            if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err))
+            if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err, P.spin_limit))
                 return false;
         }
 #pragma unroll
@@ -1045,12 +1093,12 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         const int q_in = has_interior ? WAVE : S;
         const int q_out = has_interior ? max(((M - U) / U + 1) * U, WAVE) : S;
         for (; q0 < q_in; q0 += U)
-            if (!group(q0, std::false_type{})) return;
+            if (!group(q0, std::false_type{})) return give_up_bwd(P, p, b);
         for (; q0 < q_out; q0 += U)
-            if (!group(q0, std::true_type{})) return;
+            if (!group(q0, std::true_type{})) return give_up_bwd(P, p, b);
     }
     for (; q0 < S; q0 += U)
-        if (!group(q0, std::false_type{})) return;
+        if (!group(q0, std::false_type{})) return give_up_bwd(P, p, b);
 }
 
 template <class Cost, bool BAND, bool EXACT>
@@ -1080,7 +1128,7 @@ __global__ void __launch_bounds__((dp_threads<Cost, true>())) bwd_kernel(DPParam
             producer_wave<Cost, true>(P, sm, p, g * P.W + wb, wb);
         } else {
             CostRing cost;
-            cost.bind(sm, w, P.err);
+            cost.bind(sm, w, P);
             bwd_band<CostRing, BAND, EXACT>(P, cost, sm, p, g, w);
         }
     } else {

@@ -6,6 +6,9 @@
 
 namespace sdtw {
 
+// Polls a bounded inter-wave wait makes before it gives up (about 0.3 s of no progress).
+constexpr unsigned kDefaultSpinLimit = 1u << 22;
+
 // Parameters of the wavefront kernels (forward and backward share one block).
 struct DPParams {
     const float* D;     // unfused cost (B,N,M) or nullptr
@@ -25,6 +28,7 @@ struct DPParams {
     float4* gring4;     // backward: (B*G, RW) (E, R, D, tag) first rows
     int RW;             // entries per cross-workgroup row: M plus 64 of padding each side
     int* err;           // spin-timeout flag
+    unsigned spin_limit;  // polls a bounded wait makes before it gives up (kDefaultSpinLimit)
     int B, N, M, K;
     int nb, W, G;       // 64-row bands per pair, waves per workgroup, workgroups per pair
     int S;              // steps per band in the R table (dp_band_steps(M))

@@ -8,7 +8,6 @@ missing or no GPU is present, they raise.
 from __future__ import annotations
 
 import ctypes
-import functools
 import os
 import threading
 
@@ -23,7 +22,7 @@ _lock = threading.Lock()
 
 # include/sdtw.h enums
 OP_SQEUCLID_FWD, OP_SQEUCLID_BWD, OP_FWD, OP_BWD, OP_FUSED_FWD, OP_FUSED_BWD = range(6)
-DIST_EXACT, DIST_MFMA = 0, 1
+DIST_EXACT = 0
 NUMERICS = {"fast": 0, "exact": 1, "mixed": 2}
 
 _SIGS = {
@@ -31,6 +30,8 @@ _SIGS = {
     "sdtw_version": ([], ctypes.c_int),
     "sdtw_set_numerics": ([ctypes.c_int], ctypes.c_int),
     "sdtw_get_numerics": ([], ctypes.c_int),
+    "sdtw_set_wait_limit": ([ctypes.c_uint], ctypes.c_uint),
+    "sdtw_fused_bands_per_workgroup": ([ctypes.c_int64] * 4, ctypes.c_int),
     "sdtw_workspace_bytes": ([ctypes.c_int] + [ctypes.c_int64] * 4, ctypes.c_size_t),
     "sdtw_table_elems": ([ctypes.c_int64] * 3, ctypes.c_int64),
     "sdtw_debug_status": ([ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t] + [ctypes.c_int64] * 4, ctypes.c_int),
@@ -120,6 +121,12 @@ def set_numerics(mode: str) -> str:
 
 def get_numerics() -> str:
     return {v: k for k, v in NUMERICS.items()}[load().sdtw_get_numerics()]
+
+
+def set_wait_limit(polls: int) -> int:
+    """Polls a wavefront kernel's bounded wait makes before giving up (process-wide); returns
+    the previous limit.  A test hook: a wave that gives up marks its pair's results NaN."""
+    return int(load().sdtw_set_wait_limit(int(polls)))
 
 
 def strerror(rc: int) -> str:
@@ -314,24 +321,23 @@ def fused_costs_on_matrix_cores(N: int, M: int, K: int) -> bool:
     return K <= 64 and K * N * M >= 400
 
 
-@functools.lru_cache(maxsize=None)
-def _cu_count(index: int) -> int:
-    return torch.cuda.get_device_properties(index).multi_processor_count
+def fused_bands_per_workgroup(B: int, N: int, M: int, K: int, device) -> int:
+    """The fused recursions' bands per workgroup at this shape on `device` (the library's
+    own choice, sdtw_fused_bands_per_workgroup): 2 or 4."""
+    with torch.cuda.device(device):
+        return int(load().sdtw_fused_bands_per_workgroup(B, N, M, K))
 
 
 def one_launch_unfused_forward(B: int, N: int, M: int, K: int, device) -> bool:
     """Whether sdtw_fused_fwd_d_f32 beats the distance launch plus the D-reading recursion.
-    It needs matrix-core costs, and the batch's 2-band workgroups must all fit on the GPU at
-    once (B * ceil(ceil(N/64)/2) <= CU count, the library's own choice): the producer waves
-    then have SIMDs of their own, whereas sharing their compute waves' SIMDs, the D stores
-    slow the recursion (B=32 N=M=2048 D=64: 2.78 against 2.70 ms per step).  Not under
-    "fast" arithmetic, whose short recursion step makes the storing producers the limit."""
+    It needs matrix-core costs, and the library must take its 2-band geometry (the batch's
+    2-band workgroups all fit on the GPU at once): the producer waves then have SIMDs of
+    their own, whereas sharing their compute waves' SIMDs, the D stores slow the recursion
+    (B=32 N=M=2048 D=64: 2.78 against 2.70 ms per step).  Not under "fast" arithmetic,
+    whose short recursion step makes the storing producers the limit."""
     if not fused_costs_on_matrix_cores(N, M, K) or get_numerics() == "fast":
         return False
-    bands = -(-N // 64)
-    groups = -(-bands // 2)  # workgroups per pair at 2 bands each
-    index = torch.device(device).index
-    return B * groups <= _cu_count(torch.cuda.current_device() if index is None else index)
+    return fused_bands_per_workgroup(B, N, M, K, device) == 2
 
 
 def fused_fwd_d(x, y, gamma: float, bandwidth: float):

@@ -60,24 +60,46 @@ def test_workspace_sizes():
     assert lib.sdtw_workspace_bytes(99, B, N, M, K) == 0
 
 
+def test_fused_geometry_query():
+    # the library's own choice of bands per workgroup (without a visible GPU it assumes 256
+    # CUs, the MI355X count): 2 while the batch's 2-band workgroups all fit at once
+    q = _engine.load().sdtw_fused_bands_per_workgroup
+    assert q(32, 512, 512, 64) == 2      # 32 * 4 = 128 workgroups
+    assert q(32, 1024, 1024, 64) == 2    # 32 * 8 = 256: still fits
+    assert q(32, 2048, 2048, 64) == 4    # 32 * 16 = 512
+    assert q(16, 4096, 3072, 4) == 4     # the long configuration: 16 * 32 = 512
+    assert q(256, 64, 64, 8) == 2        # one band per pair
+    assert q(257, 64, 64, 8) == 4
+    assert q(4, 512, 512, 65) == 4       # K > 64: scalar cost tiles
+    assert q(1, 5, 5, 3) == 4            # K*N*M < 400: scalar cost tiles
+    assert q(1, 0, 5, 3) == 0            # invalid shape
+
+
 def test_one_launch_unfused_forward_choice(monkeypatch):
     # the unfused module takes the one-launch forward only with matrix-core costs, in the
-    # 2-band geometry (B * ceil(ceil(N/64)/2) <= CU count) and outside "fast" arithmetic
-    monkeypatch.setattr(_engine, "_cu_count", lambda index: 256)
+    # library's 2-band geometry and outside "fast" arithmetic
+    lib = _engine.load()
+    monkeypatch.setattr(_engine, "fused_bands_per_workgroup",
+                        lambda B, N, M, K, device: lib.sdtw_fused_bands_per_workgroup(B, N, M, K))
     prev = _engine.set_numerics("mixed")
     try:
         pick = _engine.one_launch_unfused_forward
-        assert pick(32, 512, 512, 64, "cuda:0")         # 32 * 4 = 128 workgroups
-        assert pick(32, 1024, 1024, 64, "cuda:0")       # 32 * 8 = 256: still fits
-        assert not pick(32, 2048, 2048, 64, "cuda:0")   # 32 * 16 = 512: 4-band geometry
-        assert pick(256, 64, 64, 8, "cuda:0")           # one band per pair
+        assert pick(32, 512, 512, 64, "cuda:0")
+        assert pick(32, 1024, 1024, 64, "cuda:0")
+        assert not pick(32, 2048, 2048, 64, "cuda:0")
+        assert pick(256, 64, 64, 8, "cuda:0")
         assert not pick(257, 64, 64, 8, "cuda:0")
         assert pick(16, 2048, 2048, 1, "cuda:0")
-        assert not pick(4, 512, 512, 65, "cuda:0")      # K > 64: scalar cost tiles
-        assert not pick(1, 5, 5, 3, "cuda:0")           # K*N*M < 400: scalar cost tiles
+        assert not pick(4, 512, 512, 65, "cuda:0")
+        assert not pick(1, 5, 5, 3, "cuda:0")
         assert _engine.set_numerics("exact") == "mixed"
         assert pick(32, 512, 512, 64, "cuda:0")
         _engine.set_numerics("fast")
         assert not pick(32, 512, 512, 64, "cuda:0")
     finally:
         _engine.set_numerics(prev)
+
+
+def test_wait_limit_setter():
+    assert _engine.set_wait_limit(1000) == 1 << 22
+    assert _engine.set_wait_limit(1 << 22) == 1000
