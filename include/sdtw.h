@@ -40,7 +40,8 @@ typedef enum sdtw_status {
     SDTW_ERR_WORKSPACE = 2,      /* ws too small (see sdtw_workspace_bytes) */
     SDTW_ERR_LAUNCH = 3,         /* hipLaunchKernel / runtime error */
     SDTW_ERR_UNSUPPORTED = 4,    /* shape outside what the kernels support */
-    SDTW_ERR_TIMEOUT = 5         /* a bounded inter-band wait expired (results invalid) */
+    SDTW_ERR_TIMEOUT = 5,        /* a bounded inter-band wait expired (results invalid) */
+    SDTW_ERR_SCRATCH_LIMIT = 6   /* shape exceeds the no-allocation entry point's scratch */
 } sdtw_status;
 
 /* Operation selectors for sdtw_workspace_bytes. */
@@ -152,6 +153,22 @@ int sdtw_sqeuclid_bwd_f32(const float *x, const float *y, const float *D, const 
  * numerics of the reference CPU path launcher.py:307-324 (fp64 recursion, fp32 R). */
 int sdtw_fwd_f32(const float *D, float *R, float *out, int64_t B, int64_t N, int64_t M,
                  double gamma, double bandwidth, void *ws, size_t ws_bytes, void *stream);
+
+/* sdtw_fwd_f32 without a workspace argument and without any allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Its scratch (the
+ * workgroup ticket, the error flag and the cross-workgroup rows) is a static device array
+ * of sdtw_fwd_f32_noalloc_scratch_limit() bytes (16 MiB) per GPU, held until the process
+ * ends; the first call on a device looks up that device's copy.  A shape whose scratch
+ * (sdtw_workspace_bytes(SDTW_OP_FWD, B, N, M, 0)) exceeds the limit returns
+ * SDTW_ERR_SCRATCH_LIMIT before any device call.  Each call resets the scratch in a kernel
+ * launched ahead of the recursion (no memset node), so earlier contents never matter; but
+ * every call on one GPU uses the same array, so calls that overlap on one GPU (different
+ * streams, or threads) race and give wrong results: serialise them.  Results are bit-for-bit
+ * those of sdtw_fwd_f32. */
+int sdtw_fwd_f32_noalloc(const float *D, float *R, float *out, int64_t B, int64_t N, int64_t M,
+                         double gamma, double bandwidth, void *stream);
+size_t sdtw_fwd_f32_noalloc_scratch_limit(void);
 
 /* Soft-DTW backward: G[b,i,j] = gout[b] * E[b,i,j], E = d out[b] / d D[b,i,j].
  * gout may be NULL (treated as 1, i.e. G = E, what launcher.py returns).

@@ -5,11 +5,19 @@
 #include <math.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "../../include/sdtw.h"
 #include "sdtw_internal.hpp"
 
 using namespace sdtw;
+
+// Scratch of the no-allocation forward (sdtw_fwd_f32_noalloc): a file-scope device array,
+// one copy per GPU, held until the process ends.  In host code `scratch` names a host-side
+// stand-in, not device memory: its device address is taken once per device with
+// hipGetSymbolAddress (with that device current) and only that address is used.
+static constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
 
@@ -153,6 +161,24 @@ std::atomic<int> g_numerics{SDTW_NUMERICS_MIXED};
 bool exact_forward() { return g_numerics.load(std::memory_order_relaxed) != SDTW_NUMERICS_FAST; }
 bool exact_backward() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_EXACT; }
 
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch`, or nullptr on a runtime error.
+void* device_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (ptr) return ptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (ptr) return ptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    return ptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -165,11 +191,14 @@ const char* sdtw_strerror(int status) {
         case SDTW_ERR_LAUNCH: return "HIP kernel launch failed";
         case SDTW_ERR_UNSUPPORTED: return "unsupported configuration";
         case SDTW_ERR_TIMEOUT: return "a wavefront kernel gave up waiting on a neighbour band";
+        case SDTW_ERR_SCRATCH_LIMIT:
+            return "shape needs more scratch than the no-allocation entry point holds "
+                   "(sdtw_fwd_f32_noalloc_scratch_limit); use sdtw_fwd_f32 with a workspace";
         default: return "unknown sdtw status";
     }
 }
 
-int sdtw_version(void) { return 5; }
+int sdtw_version(void) { return 6; }
 
 int sdtw_set_numerics(int mode) {
     if (mode != SDTW_NUMERICS_FAST && mode != SDTW_NUMERICS_EXACT && mode != SDTW_NUMERICS_MIXED)
@@ -321,6 +350,25 @@ int sdtw_fwd_f32(const float* D, float* R, float* out, int64_t B, int64_t N, int
     p.R = R;
     p.out = out;
     return status_of(launch_fwd(p, false, false, exact_forward(), (hipStream_t)stream));
+}
+
+size_t sdtw_fwd_f32_noalloc_scratch_limit(void) { return kNoAllocScratchBytes; }
+
+int sdtw_fwd_f32_noalloc(const float* D, float* R, float* out, int64_t B, int64_t N, int64_t M,
+                         double gamma, double bandwidth, void* stream) {
+    if (!shape_ok(B, N, M, 1, false) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0) return SDTW_OK;
+    if (!D || !R || !out) return SDTW_ERR_INVALID_VALUE;
+    // the size check comes before any runtime call (in 128 bits: no shape wraps it round)
+    const DPGeom g = dp_geom(N);
+    const unsigned __int128 need =
+        256 + (unsigned __int128)16 * (unsigned __int128)B * g.G * dp_row_entries(M);
+    if (need > kNoAllocScratchBytes) return SDTW_ERR_SCRATCH_LIMIT;
+    void* ws = device_scratch();
+    if (!ws) return SDTW_ERR_LAUNCH;
+    // the prep launch that precedes the recursion resets the ticket and the error flag and
+    // empties the cross-workgroup rows, so nothing of an earlier call's contents is read
+    return sdtw_fwd_f32(D, R, out, B, N, M, gamma, bandwidth, ws, kNoAllocScratchBytes, stream);
 }
 
 int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, int64_t B,

@@ -46,6 +46,9 @@ _SIGS = {
     "sdtw_fwd_f32": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3
                      + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                      ctypes.c_int),
+    "sdtw_fwd_f32_noalloc": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3
+                             + [ctypes.c_double] * 2 + [ctypes.c_void_p], ctypes.c_int),
+    "sdtw_fwd_f32_noalloc_scratch_limit": ([], ctypes.c_size_t),
     "sdtw_bwd_f32": ([ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3
                      + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                      ctypes.c_int),
@@ -276,6 +279,27 @@ def dtw_fwd(D: torch.Tensor, gamma: float, bandwidth: float):
                                  float(bandwidth), _ptr(ws), nws, _stream(D.device))
     _check(rc, "softdtw forward")
     _debug_check(OP_FWD, ws, nws, B, N, M, 0, "softdtw forward")
+    return out, R
+
+
+def dtw_fwd_noalloc(D: torch.Tensor, gamma: float, bandwidth: float, R=None, out=None):
+    """sdtw_fwd_f32_noalloc: the forward of dtw_fwd with the library's static scratch instead
+    of a workspace.  R and out may be passed in (preallocated); they are returned."""
+    require_gpu(D, "softdtw forward D")
+    _check_shapes(D=D)
+    B, N, M = D.shape
+    if R is None:
+        R = torch.empty((table_elems(B, N, M),), dtype=torch.float32, device=D.device)
+    if out is None:
+        out = torch.empty((B,), dtype=torch.float32, device=D.device)
+    require_gpu(R, "softdtw forward R")
+    require_gpu(out, "softdtw forward out")
+    if R.numel() != table_elems(B, N, M) or out.numel() != B:
+        raise ValueError("softdtw_cuda: R / out sizes do not match (B, N, M)")
+    with torch.cuda.device(D.device):
+        rc = load().sdtw_fwd_f32_noalloc(_ptr(D), _ptr(R), _ptr(out), B, N, M, float(gamma),
+                                         float(bandwidth), _stream(D.device))
+    _check(rc, "softdtw forward (no allocation)")
     return out, R
 
 

@@ -103,3 +103,15 @@ def test_one_launch_unfused_forward_choice(monkeypatch):
 def test_wait_limit_setter():
     assert _engine.set_wait_limit(1000) == 1 << 22
     assert _engine.set_wait_limit(1 << 22) == 1000
+
+
+def test_noalloc_forward_limit_checked_before_any_device_call():
+    # the size check returns before the runtime is touched, so it answers without a GPU
+    lib = _engine.load()
+    assert lib.sdtw_fwd_f32_noalloc_scratch_limit() == 16 << 20
+    fake = ctypes.c_void_p(256)  # never dereferenced
+    assert lib.sdtw_fwd_f32_noalloc(fake, fake, fake, 64, 4096, 8192, 1.0, -1.0, None) == 6
+    assert lib.sdtw_fwd_f32_noalloc(fake, fake, fake, 1, 0, 8, 1.0, -1.0, None) == 1
+    assert lib.sdtw_fwd_f32_noalloc(fake, fake, fake, 0, 8, 8, 1.0, -1.0, None) == 0
+    # the largest batch of the long configuration's shape that fits: 16 * 16 * 3200 * 16 B
+    assert lib.sdtw_workspace_bytes(_engine.OP_FWD, 16, 4096, 3072, 0) <= 16 << 20
