@@ -196,6 +196,22 @@ SDTW_DEV double fwd_cell_exact(double R0, double R1, double R2, float d, double 
     return fma(-gamma, fm::log_tab_1to3(rsum, L), ((double)d + m) + nanfix);
 }
 
+// fwd_cell_exact for finite inputs with a finite minimum, in fewer instructions: the minimum,
+// median and maximum of the predecessors come from a min/max network (the sum of the two
+// non-minimum terms does not depend on their order), and no NaN is restored.  Where those
+// conditions hold it returns fwd_cell_exact's bits.  The forward takes it only while every
+// cost the band uses and every value the band above hands over is finite; then each active
+// cell has a finite predecessor (the diagonal one, or the left one in row 0, or R[0,0]).
+SDTW_DEV double fwd_cell_exact_finite(double R0, double R1, double R2, float d, double gamma,
+                                      double inv_gamma, const double* T, const double* L) {
+    const double lo = fmin(R0, R2), hi = fmax(R0, R2);
+    const double m = fmin(lo, R1), mx = fmax(hi, R1), md = fmax(lo, fmin(hi, R1));
+    const double ea = fm::exp_tab_abs((m - md) * inv_gamma, T);
+    const double eb = fm::exp_tab_abs((m - mx) * inv_gamma, T);
+    const double rsum = (ea + eb) + 1.0;
+    return fma(-gamma, fm::log_tab_1to3(rsum, L), (double)d + m);
+}
+
 // One backward cell (launcher.py:347-351): fp32 differences, fp64 exp/products/sum (in the
 // reference's order), E rounded to fp32.  The exponential's clamp drops NaN, which is put
 // back explicitly.
@@ -754,39 +770,73 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 #pragma unroll
     for (int u = 0; u < U; ++u) d_nxt[u] = crow[(u - l) & (CR - 1)];
 
-    for (int s0 = 0; s0 < S; s0 += U) {
+    // One group of U steps from s0.  Returns 0, -1 if a wait expired, or 1 (FINITE bodies
+    // only) if the group's inputs are not all finite: nothing has been computed then, and
+    // the caller runs the group again, and the rest of the band, with the general cell.
+    // Every step of the group start is idempotent (copies, waits, counter publications of
+    // the same values), so running it twice is harmless.
+    //   FINITE: fwd_cell_exact_finite, valid while every cost this lane uses and every entry
+    //     of the band above that lane 0 uses is finite (checked here per group; the cost
+    //     rings start zeroed, so slots never written hold finite values too);
+    //   INTERIOR: every lane is inside the table for all U steps (a full band, columns
+    //     s0 - 63 .. s0 + U - 1 within [0, M)), so no step needs the inactive masking.
+    // Separate loops run the bodies (a branch per group between two unrolled bodies would
+    // join their loop-carried registers).
+    auto group = [&](int s0, auto finite_tag, auto interior_tag) -> int {
+        constexpr bool FINITE = decltype(finite_tag)::value;
+        constexpr bool INTERIOR = decltype(interior_tag)::value;
 #pragma unroll
         for (int u = 0; u < U; ++u) d_cur[u] = d_nxt[u];
-        if (!cost.begin(cring, s0 + 2 * TC) || !fetch_lds(s0, up_cur)) {
-            give_up_fwd(P, p);
-            return;
+        if (!cost.begin(cring, s0 + 2 * TC) || !fetch_lds(s0, up_cur)) return -1;
+        if constexpr (FINITE) {
+            float cs = d_cur[0];
+#pragma unroll
+            for (int u = 1; u < U; ++u) cs += d_cur[u];
+            bool bad = !(fabsf(cs) < __builtin_inff());  // a NaN or an infinity among them
+            if (b > 0) {  // band 0's input is the +inf padding row
+                double us = 0.0;
+                if (s0 + U <= M) {
+#pragma unroll
+                    for (int u = 0; u < U; ++u) us += up_cur[u];
+                } else {  // the last groups: only columns below M are used
+#pragma unroll
+                    for (int u = 0; u < U; ++u) us += (s0 + u < M) ? up_cur[u] : 0.0;
+                }
+                bad = bad || !(fabs(us) < dinf());
+            }
+            if (__builtin_amdgcn_ballot_w64(bad)) return 1;
         }
         // this group writes columns up to s0 + U - 64 of my last row; writing column c
         // reuses the slot of column c - RS, which the consumer must have taken
         if (out_lds) {
             const int need_free = s0 + U - WAVE + 1 - RS;
-            if (need_free > 0 && !wait_at_least(sm.cons() + (w + 1), need_free, known_free, P.err, P.spin_limit)) {
-                give_up_fwd(P, p);
-                return;
-            }
+            if (need_free > 0 && !wait_at_least(sm.cons() + (w + 1), need_free, known_free, P.err, P.spin_limit))
+                return -1;
         }
         float* Rg = Rt + (int64_t)s0 * WAVE;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = s0 + u - l;
-            const bool act = row_ok && (unsigned)j < (unsigned)M;
-            bool keep = act;
-            if (BAND) keep = keep && !out_of_band(bw, i, j);
             const double up = shr1(up_cur[u], prev);
-            double cand;
-            if (EXACT) {
-                cand = fwd_cell_exact(diag, up, left, d_cur[u], gamma, inv_gamma, tabE, tabL);
+            double r;
+            if constexpr (INTERIOR) {
+                r = fwd_cell_exact_finite(diag, up, left, d_cur[u], gamma, inv_gamma, tabE, tabL);
             } else {
-                cand = fwd_cell_hw(diag, up, left, d_cur[u], c2, ngl);
+                const int j = s0 + u - l;
+                const bool act = row_ok && (unsigned)j < (unsigned)M;
+                bool keep = act;
+                if (BAND) keep = keep && !out_of_band(bw, i, j);
+                double cand;
+                if constexpr (FINITE) {
+                    cand = fwd_cell_exact_finite(diag, up, left, d_cur[u], gamma, inv_gamma, tabE, tabL);
+                } else if (EXACT) {
+                    cand = fwd_cell_exact(diag, up, left, d_cur[u], gamma, inv_gamma, tabE, tabL);
+                } else {
+                    cand = fwd_cell_hw(diag, up, left, d_cur[u], c2, ngl);
+                }
+                // inactive lanes publish +inf: before its first column a lane's left/up are
+                // the +inf padding, out-of-band cells stay +inf (launcher.py:310, :315)
+                r = keep ? cand : INF;
             }
-            // inactive lanes publish +inf: before its first column a lane's left/up are the
-            // +inf padding, out-of-band cells stay +inf (launcher.py:310, :315)
-            const double r = keep ? cand : INF;
             left = r;
             diag = up;
             prev = r;
@@ -798,7 +848,32 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         }
         cost.end(cring, s0 + 2 * TC, s0 + 3 * TC);
         if (out_lds || out_glb) handover(s0);
+        return 0;
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    int s0 = 0;
+    int rc = 0;
+    if constexpr (EXACT && !BAND) {
+        // interior groups: s0 >= 64 (column s0 - 63 > 0 for lane 63) and s0 + U <= M, in a
+        // full band
+        const bool full = (b + 1) * WAVE <= N;
+        const int q_in = min(full ? WAVE : S, S);
+        const int q_out = full ? max((M - U) / U * U + U, WAVE) : S;
+        for (; s0 < q_in; s0 += U)
+            if ((rc = group(s0, T_{}, F_{})) != 0) break;
+        if (rc == 0)
+            for (; s0 < min(q_out, S); s0 += U)
+                if ((rc = group(s0, T_{}, T_{})) != 0) break;
+        if (rc == 0)
+            for (; s0 < S; s0 += U)
+                if ((rc = group(s0, T_{}, F_{})) != 0) break;
+        if (rc < 0) return give_up_fwd(P, p);
     }
+    // the general cell: the band, the fast arithmetic, and a band whose inputs are not all
+    // finite (from the group that found it, s0, onwards)
+    for (; s0 < S; s0 += U)
+        if (group(s0, F_{}, F_{}) < 0) return give_up_fwd(P, p);
     // out[p] = R[N-1, M-1] as stored (step M-1+l of this lane, written by this lane)
     if (i == N - 1) P.out[p] = Rt[(int64_t)(M - 1 + l) * WAVE];
 }
@@ -866,6 +941,12 @@ __global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPPara
     // ring 0 starts at +inf: the padding row above band 0 (the helper wave overwrites it
     // in workgroups that have a band above them)
     for (int e = threadIdx.x; e < RS; e += blockDim.x) reinterpret_cast<double*>(sm.ring())[e] = dinf();
+    // the cost rings start zeroed where the finite-input check reads them (slots of columns
+    // outside the table that no tile has written yet must not hold a non-finite pattern)
+    if (EXACT && !BAND) {
+        float4* cr = reinterpret_cast<float4*>(sm.cost_ring(0));
+        for (int e = threadIdx.x; e < P.W * WAVE * CS / 4; e += blockDim.x) cr[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G, g = t - p * P.G;

@@ -242,3 +242,55 @@ def test_unfused_normalize_matches_two_node_graph():
     torch.testing.assert_close(out_a, out_b, rtol=1e-6, atol=1e-5)
     torch.testing.assert_close(xa.grad, xb.grad, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(ya.grad, yb.grad, rtol=1e-5, atol=1e-6)
+
+
+def _same_R(Rc, Ro):
+    """R tables equal as the CPU path leaves them: NaN where it has NaN, the same infinities,
+    and every finite value with the same bits."""
+    assert torch.equal(torch.isnan(Rc), torch.isnan(Ro)), "NaN pattern differs"
+    fin = ~torch.isnan(Ro)
+    assert torch.equal(Rc[fin], Ro[fin]), "values differ"
+
+
+@pytest.mark.parametrize("mode", ["exact", "mixed"])
+@pytest.mark.parametrize("N,M", [(200, 150), (700, 180)])
+def test_dp_forward_nonfinite_costs_vs_oracle(N, M, mode):
+    """Costs with NaN and +inf entries in chosen bands.  The forward runs a band with the
+    finite-input cell only while its inputs are finite, and switches to the general cell
+    (NaN restored, all-+inf predecessors give NaN as in the reference) from the group that
+    first sees a non-finite cost or a non-finite entry of the band above; at 700 rows the
+    entries also cross workgroups through the helper wave."""
+    say(f"[dp nonfinite] {mode} N={N} M={M}")
+    B = 4
+    x, y = randn_pair(B, N, M, 3, seed=N + 7)
+    D = oracle.sqeuclidean(x, y)
+    D[0, N // 2, M // 3] = float("nan")          # a NaN in a middle band
+    D[1, 5, 5] = float("inf")                    # +inf in band 0
+    D[1, N - 40, 2] = float("inf")               # and in the last band, near the left edge
+    D[2, 63, 10] = float("inf")                  # the last row of band 0: crosses to band 1
+    D[2, 0, M - 1] = float("nan")                # top-right corner: reaches only column M - 1
+    # pair 3 stays finite
+    out_o, R_o = oracle.forward(D, 1.0, None)
+    with numerics(mode):
+        out, R = _engine.dtw_fwd(D.cuda(), 1.0, -1.0)
+    Rc = _engine.table_unpack(R, B, N, M).cpu()
+    _same_R(Rc, engine_R_from_oracle(R_o))
+    _same_R(out.cpu(), out_o)
+    # the NaN spreads to every cell after it; an infinite cost leaves only its own cell
+    # infinite (its neighbours keep a finite predecessor)
+    assert torch.isnan(Rc[0]).any() and torch.isposinf(Rc[1]).any() and torch.isfinite(Rc[3]).all()
+
+
+def test_fused_forward_nonfinite_inputs_vs_oracle():
+    """x with a NaN feature and an infinite one: the producer waves' cost tiles carry them,
+    and the recursion switches to the general cell as in the unfused forward."""
+    B, N, M, K = 3, 300, 260, 8
+    x, y = randn_pair(B, N, M, K, seed=11)
+    x[0, 150, 2] = float("nan")
+    x[1, 70, 0] = float("inf")
+    D = oracle.sqeuclidean(x, y)
+    out_o, R_o = oracle.forward(D, 0.5, None)
+    out, R = _engine.fused_fwd(x.cuda(), y.cuda(), 0.5, -1.0)
+    Rc = _engine.table_unpack(R, B, N, M).cpu()
+    _same_R(Rc, engine_R_from_oracle(R_o))
+    _same_R(out.cpu(), out_o)
