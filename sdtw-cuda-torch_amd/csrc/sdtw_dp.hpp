@@ -277,6 +277,9 @@ SDTW_DEV float bwd_cell_hw(float rij, float En, float Rn, float Dn, float Er, fl
 constexpr int CR = 128;  // ring columns (power of two)
 constexpr int CS = 144;  // row stride in floats: CS mod 64 = 16 (tile writes by 4-row
                          // groups hit disjoint banks), CS - 1 odd (diagonal reads)
+// Slots CR .. CR + U - 1 of every row mirror slots 0 .. U - 1 (every tile store writes both),
+// so a lane reads U consecutive columns from slot c & (CR - 1) on with immediate offsets,
+// without wrapping the index per column.
 constexpr int TC = U;    // tile columns per group
 
 // Unfused: the tile is read from the (B, N, M) cost.  Lane l loads column c0 + (l & 15)
@@ -304,9 +307,14 @@ struct CostD {
     // write the loaded tile c0 into the ring
     SDTW_DEV void store(float* ring, int c0) {
         const int l = threadIdx.x & (WAVE - 1);
-        float* dst = ring + (l >> 4) * CS + ((c0 + (l & 15)) & (CR - 1));
+        const int sl = (c0 + (l & 15)) & (CR - 1);
+        float* dst = ring + (l >> 4) * CS + sl;
 #pragma unroll
         for (int k = 0; k < 16; ++k) dst[4 * k * CS] = v[k];
+        if (sl < U) {  // the mirror slots
+#pragma unroll
+            for (int k = 0; k < 16; ++k) dst[4 * k * CS + CR] = v[k];
+        }
     }
     SDTW_DEV bool prologue(float* ring, int c) {
         issue(c);
@@ -417,12 +425,17 @@ struct CostMfma {
     }
     SDTW_DEV void finish(float* ring, int c0) {
         const int l = threadIdx.x & (WAVE - 1);
-        float* dst = ring + 4 * (l >> 4) * CS + ((c0 + (l & 15)) & (CR - 1));
+        const int sl = (c0 + (l & 15)) & (CR - 1);
+        float* dst = ring + 4 * (l >> 4) * CS + sl;
+        const bool mir = sl < U;  // the mirror slots
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                dst[(16 * rb + r) * CS] = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
+            for (int r = 0; r < 4; ++r) {
+                const float v = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
+                dst[(16 * rb + r) * CS] = v;
+                if (mir) dst[(16 * rb + r) * CS + CR] = v;
+            }
     }
     // the same tile into the pair's cost tensor Dp (N, M): lane l's column c0 + (l & 15) of
     // rows row0 + 16 rb + 4 (l >> 4) + r, 16 lanes per 64-byte row segment
@@ -472,14 +485,17 @@ struct CostScalar {
         const int l = threadIdx.x & (WAVE - 1);
         const int col = min(max(c0 + (l & 15), 0), M - 1);
         const float* yj = y + (int64_t)col * K;
-        float* dst = ring + (l >> 4) * CS + ((c0 + (l & 15)) & (CR - 1));
+        const int sl = (c0 + (l & 15)) & (CR - 1);
+        float* dst = ring + (l >> 4) * CS + sl;
         for (int k4 = 0; k4 < 16; ++k4) {
             const int row = min(row0 + 4 * k4 + (l >> 4), N - 1);
             const float* xi = x + (int64_t)row * K;
             float acc = 0.0f;
             for (int k = 0; k < K; ++k)
                 acc = MULADD ? __fadd_rn(acc, __fmul_rn(xi[k], yj[k])) : __fmaf_rn(xi[k], yj[k], acc);
-            dst[4 * k4 * CS] = clamp0(exact_cost_pre(x2[row], y2[col], acc));
+            const float v = clamp0(exact_cost_pre(x2[row], y2[col], acc));
+            dst[4 * k4 * CS] = v;
+            if (sl < U) dst[4 * k4 * CS + CR] = v;  // the mirror slots
         }
     }
 };
@@ -767,8 +783,11 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         return;
     }
     cost.preload(2 * TC);
+    {
+        const float* dn = crow + ((-l) & (CR - 1));  // U consecutive slots (mirrored past CR)
 #pragma unroll
-    for (int u = 0; u < U; ++u) d_nxt[u] = crow[(u - l) & (CR - 1)];
+        for (int u = 0; u < U; ++u) d_nxt[u] = dn[u];
+    }
 
     // One group of U steps from s0.  Returns 0, -1 if a wait expired, or 1 (FINITE bodies
     // only) if the group's inputs are not all finite: nothing has been computed then, and
@@ -814,6 +833,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
                 return -1;
         }
         float* Rg = Rt + (int64_t)s0 * WAVE;
+        const float* dn = crow + ((s0 + TC - l) & (CR - 1));  // next group's costs
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const double up = shr1(up_cur[u], prev);
@@ -843,7 +863,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             cap = shl1(r, cap);
             Rg[u * WAVE] = (float)r;
             // next group's costs, and the tile work, between the steps
-            d_nxt[u] = crow[(s0 + TC + u - l) & (CR - 1)];
+            d_nxt[u] = dn[u];
             cost.step(u, s0 + 2 * TC, s0 + 3 * TC);
         }
         cost.end(cring, s0 + 2 * TC, s0 + 3 * TC);
