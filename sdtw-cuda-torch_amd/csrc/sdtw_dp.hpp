@@ -288,13 +288,16 @@ constexpr int TC = U;    // tile columns per group
 struct CostD {
     const float* base;  // this pair's cost
     int M, row0, N;
+    int badc;           // first column of a stored tile holding a non-finite cost (or INT_MAX)
     float v[16];
     SDTW_DEV void init(const DPParams& P, int p, int b) {
         M = P.M;
         N = P.N;
         base = P.D + (int64_t)p * P.N * P.M;
         row0 = b * WAVE;
+        badc = INT_MAX;
     }
+    SDTW_DEV int first_bad_col() const { return badc; }
     SDTW_DEV void issue(int c0) {
         const int l = threadIdx.x & (WAVE - 1);
         const int col = min(max(c0 + (l & 15), 0), M - 1);
@@ -309,12 +312,17 @@ struct CostD {
         const int l = threadIdx.x & (WAVE - 1);
         const int sl = (c0 + (l & 15)) & (CR - 1);
         float* dst = ring + (l >> 4) * CS + sl;
+        float sum = 0.0f;  // NaN or infinite if a cost is
 #pragma unroll
-        for (int k = 0; k < 16; ++k) dst[4 * k * CS] = v[k];
+        for (int k = 0; k < 16; ++k) {
+            dst[4 * k * CS] = v[k];
+            sum += v[k];
+        }
         if (sl < U) {  // the mirror slots
 #pragma unroll
             for (int k = 0; k < 16; ++k) dst[4 * k * CS + CR] = v[k];
         }
+        if (__builtin_amdgcn_ballot_w64(!(fabsf(sum) < __builtin_inff()))) badc = min(badc, c0);
     }
     SDTW_DEV bool prologue(float* ring, int c) {
         issue(c);
@@ -354,6 +362,7 @@ struct CostMfma {
     float x2o[4][4];   // norms of the output rows row0 + 16 rb + 4 (l >> 4) + r
     float yb[NKK];     // B: y[c0 + (l & 15)][4 kk + (l >> 4)]
     float y2n, y2c;    // norm of the issued / the begun tile's column
+    bool tile_bad;     // the last finished tile holds a non-finite cost (wave-uniform)
     floatx4 acc[4];
     SDTW_DEV void init(const DPParams& P, int p, int b) {
         const int l = threadIdx.x & (WAVE - 1);
@@ -428,6 +437,7 @@ struct CostMfma {
         const int sl = (c0 + (l & 15)) & (CR - 1);
         float* dst = ring + 4 * (l >> 4) * CS + sl;
         const bool mir = sl < U;  // the mirror slots
+        float sum = 0.0f;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -435,7 +445,9 @@ struct CostMfma {
                 const float v = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
                 dst[(16 * rb + r) * CS] = v;
                 if (mir) dst[(16 * rb + r) * CS + CR] = v;
+                sum += v;
             }
+        tile_bad = __builtin_amdgcn_ballot_w64(!(fabsf(sum) < __builtin_inff())) != 0;
     }
     // the same tile into the pair's cost tensor Dp (N, M): lane l's column c0 + (l & 15) of
     // rows row0 + 16 rb + 4 (l >> 4) + r, 16 lanes per 64-byte row segment
@@ -463,11 +475,14 @@ struct CostScalar {
     const float* x2;
     const float* y2;
     int M, N, K, row0;
+    int badc;  // first column of a finished tile holding a non-finite cost (or INT_MAX)
+    SDTW_DEV int first_bad_col() const { return badc; }
     SDTW_DEV void init(const DPParams& P, int p, int b) {
         M = P.M;
         N = P.N;
         K = P.K;
         row0 = b * WAVE;
+        badc = INT_MAX;
         x = P.x + (int64_t)p * N * K;
         y = P.y + (int64_t)p * M * K;
         x2 = P.x2 + (int64_t)p * N;
@@ -487,6 +502,7 @@ struct CostScalar {
         const float* yj = y + (int64_t)col * K;
         const int sl = (c0 + (l & 15)) & (CR - 1);
         float* dst = ring + (l >> 4) * CS + sl;
+        float sum = 0.0f;
         for (int k4 = 0; k4 < 16; ++k4) {
             const int row = min(row0 + 4 * k4 + (l >> 4), N - 1);
             const float* xi = x + (int64_t)row * K;
@@ -496,7 +512,9 @@ struct CostScalar {
             const float v = clamp0(exact_cost_pre(x2[row], y2[col], acc));
             dst[4 * k4 * CS] = v;
             if (sl < U) dst[4 * k4 * CS + CR] = v;  // the mirror slots
+            sum += v;
         }
+        if (__builtin_amdgcn_ballot_w64(!(fabsf(sum) < __builtin_inff()))) badc = min(badc, c0);
     }
 };
 
@@ -529,8 +547,11 @@ struct CostRing {
     const int* ready;
     int* done;
     int* err;
+    const int* badc;  // first column of a produced tile holding a non-finite cost (LDS)
     unsigned limit;
     int known, groups, pro;
+    // read after the wait for the tiles a group uses: their producer stores it first
+    SDTW_DEV int first_bad_col() const { return __builtin_amdgcn_readfirstlane(lds_load(badc)); }
     SDTW_DEV void bind(const Smem& sm, int w, const DPParams& P);
     SDTW_DEV void init(const DPParams&, int, int) {}
     // false: the wait expired (flag raised); the compute wave then stops
@@ -565,6 +586,11 @@ struct Smem {
     // band's compute wave (8 + 8 ints from int 16 of the header)
     SDTW_DEV int* ready() const { return reinterpret_cast<int*>(base) + 16; }
     SDTW_DEV int* done() const { return reinterpret_cast<int*>(base) + 24; }
+    // forward, finite-input cell: ring k's producer (band k - 1, or the helper wave for
+    // ring 0) no longer hands over values of the finite-input cell (ints 32 .. 36); the first
+    // column of a produced cost tile holding a non-finite cost, per band (ints 40 .. 43)
+    SDTW_DEV int* poison_in() const { return reinterpret_cast<int*>(base) + 32; }
+    SDTW_DEV int* bad_col() const { return reinterpret_cast<int*>(base) + 40; }
     SDTW_DEV double* tables() const { return reinterpret_cast<double*>(base + 256); }
     SDTW_DEV unsigned char* ring() const { return base + 256 + tab_bytes; }
     SDTW_DEV float* cost_ring(int w) const {
@@ -581,6 +607,7 @@ struct Smem {
 SDTW_DEV void CostRing::bind(const Smem& sm, int w, const DPParams& P) {
     ready = sm.ready() + w;
     done = sm.done() + w;
+    badc = sm.bad_col() + w;
     err = P.err;
     limit = P.spin_limit;
     known = 0;
@@ -643,6 +670,7 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
     const int* done = sm.done() + w;
     int* ready = sm.ready() + w;
     int known = 0;
+    bool marked = false;  // the band's first non-finite cost tile has been published
     const int groups = P.S / U;  // groups of the compute wave
     const int T = groups + 1;    // tiles it reads
     auto col = [&](int t) { return BWD ? P.M - TC * (t + 1) : TC * t; };
@@ -663,6 +691,13 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
         if (flush) gt.read(P, ring, (t - 4) * U);
         if constexpr (MMA) c.finish(ring, col(t));
         else c.store(ring, col(t));
+        if constexpr (MMA && !BWD) {
+            // the compute wave reads this after waiting for the tile: published first
+            if (c.tile_bad && !marked) {
+                marked = true;
+                if ((threadIdx.x & (WAVE - 1)) == 0) lds_publish(sm.bad_col() + w, col(t));
+            }
+        }
         if ((threadIdx.x & (WAVE - 1)) == 0) lds_publish(ready, t + 1);
         if (t + 1 < T) c.issue(col(t + 1));
         // unfused mode's cost tensor, from the same tile (forward; after the next loads, so
@@ -794,9 +829,9 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // the caller runs the group again, and the rest of the band, with the general cell.
     // Every step of the group start is idempotent (copies, waits, counter publications of
     // the same values), so running it twice is harmless.
-    //   FINITE: fwd_cell_exact_finite, valid while every cost this lane uses and every entry
-    //     of the band above that lane 0 uses is finite (checked here per group; the cost
-    //     rings start zeroed, so slots never written hold finite values too);
+    //   FINITE: fwd_cell_exact_finite, valid while every cost the band uses and every entry
+    //     of the band above that lane 0 uses is finite (checked here per group through flags
+    //     that the cost providers, the band above and the helper wave keep);
     //   INTERIOR: every lane is inside the table for all U steps (a full band, columns
     //     s0 - 63 .. s0 + U - 1 within [0, M)), so no step needs the inactive masking.
     // Separate loops run the bodies (a branch per group between two unrolled bodies would
@@ -808,22 +843,13 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         for (int u = 0; u < U; ++u) d_cur[u] = d_nxt[u];
         if (!cost.begin(cring, s0 + 2 * TC) || !fetch_lds(s0, up_cur)) return -1;
         if constexpr (FINITE) {
-            float cs = d_cur[0];
-#pragma unroll
-            for (int u = 1; u < U; ++u) cs += d_cur[u];
-            bool bad = !(fabsf(cs) < __builtin_inff());  // a NaN or an infinity among them
-            if (b > 0) {  // band 0's input is the +inf padding row
-                double us = 0.0;
-                if (s0 + U <= M) {
-#pragma unroll
-                    for (int u = 0; u < U; ++u) us += up_cur[u];
-                } else {  // the last groups: only columns below M are used
-#pragma unroll
-                    for (int u = 0; u < U; ++u) us += (s0 + u < M) ? up_cur[u] : 0.0;
-                }
-                bad = bad || !(fabs(us) < dinf());
-            }
-            if (__builtin_amdgcn_ballot_w64(bad)) return 1;
+            // the group's costs reach column s0 + U - 1; the band above's entries come from a
+            // band that has left the finite-input cell, or (across workgroups) were seen
+            // non-finite by the helper wave: both flags are stored before the counts this
+            // group has waited for
+            bool bad = cost.first_bad_col() <= s0 + U - 1;
+            if (b > 0) bad = bad || __builtin_amdgcn_readfirstlane(lds_load(sm.poison_in() + w)) != 0;
+            if (bad) return 1;
         }
         // this group writes columns up to s0 + U - 64 of my last row; writing column c
         // reuses the slot of column c - RS, which the consumer must have taken
@@ -889,6 +915,9 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             for (; s0 < S; s0 += U)
                 if ((rc = group(s0, T_{}, F_{})) != 0) break;
         if (rc < 0) return give_up_fwd(P, p);
+        // the band below (same workgroup) leaves the finite-input cell before it reads a
+        // value of this band's general cell
+        if (rc == 1 && out_lds && l == 0) lds_publish(sm.poison_in() + (w + 1), 1);
     }
     // the general cell: the band, the fast arithmetic, and a band whose inputs are not all
     // finite (from the group that found it, s0, onwards)
@@ -925,6 +954,12 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
         const unsigned long long miss = __ballot(empty);
         const int n = miss ? (int)__builtin_ctzll(miss) : WAVE;  // leading written entries
         if (l < n && e < M) ring[hslot(e)] = v;
+        if constexpr (std::is_same<T, double>::value) {
+            // a non-finite entry: the consumer band must leave the finite-input cell before
+            // it reads this one (flag stored before the count that covers it)
+            const bool nf = l < n && e < M && !(fabs(v) < dinf());
+            if (__builtin_amdgcn_ballot_w64(nf) && l == 0) lds_publish(sm.poison_in() + k, 1);
+        }
         if (n > 0) {
             c = min(c + n, M);
             if (l == 0) lds_publish(sm.prod() + k, c);
@@ -957,16 +992,14 @@ __global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPPara
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;  // prod and cons are contiguous
     if (threadIdx.x < 16) sm.ready()[threadIdx.x] = 0;            // ready and done likewise
+    if (threadIdx.x < 8) {
+        sm.poison_in()[threadIdx.x] = 0;
+        sm.bad_col()[threadIdx.x] = INT_MAX;
+    }
     sm.load_tables();
     // ring 0 starts at +inf: the padding row above band 0 (the helper wave overwrites it
     // in workgroups that have a band above them)
     for (int e = threadIdx.x; e < RS; e += blockDim.x) reinterpret_cast<double*>(sm.ring())[e] = dinf();
-    // the cost rings start zeroed where the finite-input check reads them (slots of columns
-    // outside the table that no tile has written yet must not hold a non-finite pattern)
-    if (EXACT && !BAND) {
-        float4* cr = reinterpret_cast<float4*>(sm.cost_ring(0));
-        for (int e = threadIdx.x; e < P.W * WAVE * CS / 4; e += blockDim.x) cr[e] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G, g = t - p * P.G;
