@@ -298,6 +298,7 @@ struct CostD {
         badc = INT_MAX;
     }
     SDTW_DEV int first_bad_col() const { return badc; }
+    SDTW_DEV int bad_col_raw() const { return badc; }
     SDTW_DEV void issue(int c0) {
         const int l = threadIdx.x & (WAVE - 1);
         const int col = min(max(c0 + (l & 15), 0), M - 1);
@@ -477,6 +478,7 @@ struct CostScalar {
     int M, N, K, row0;
     int badc;  // first column of a finished tile holding a non-finite cost (or INT_MAX)
     SDTW_DEV int first_bad_col() const { return badc; }
+    SDTW_DEV int bad_col_raw() const { return badc; }
     SDTW_DEV void init(const DPParams& P, int p, int b) {
         M = P.M;
         N = P.N;
@@ -552,6 +554,7 @@ struct CostRing {
     int known, groups, pro;
     // read after the wait for the tiles a group uses: their producer stores it first
     SDTW_DEV int first_bad_col() const { return __builtin_amdgcn_readfirstlane(lds_load(badc)); }
+    SDTW_DEV int bad_col_raw() const { return lds_load(badc); }  // the load only
     SDTW_DEV void bind(const Smem& sm, int w, const DPParams& P);
     SDTW_DEV void init(const DPParams&, int, int) {}
     // false: the wait expired (flag raised); the compute wave then stops
@@ -772,10 +775,24 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // Band above: columns [c0, c0 + U) of its last row from the LDS ring, for lane 0.  The
     // ring is read whether or not it waits: band 0's ring holds +inf throughout (set at
     // kernel start, never written), and past column M - 1 lane 0 is inactive.
-    auto fetch_lds = [&](int c0, double* dst) -> bool {
+    // The finite-input flags are read in the same LDS round trip as the count (each is stored
+    // before the count it guards): pz, the band above no longer hands over finite-cell values;
+    // bc, the first column of a cost tile with a non-finite cost (read after the cost wait).
+    auto fetch_lds = [&](int c0, double* dst, int& pz, int& bc) -> bool {
         const bool live = b > 0 && c0 < M;
         const int need = min(c0 + U, M);
-        if (live && !wait_at_least(lin_flag, need, known_in, P.err, P.spin_limit)) return false;
+        int cnt = lds_load(lin_flag);
+        pz = lds_load(sm.poison_in() + w);
+        bc = cost.bad_col_raw();
+        cnt = __builtin_amdgcn_readfirstlane(cnt);
+        pz = __builtin_amdgcn_readfirstlane(pz);
+        bc = __builtin_amdgcn_readfirstlane(bc);
+        known_in = max(known_in, cnt);
+        if (live && known_in < need) {
+            if (!wait_at_least(lin_flag, need, known_in, P.err, P.spin_limit)) return false;
+            pz = __builtin_amdgcn_readfirstlane(lds_load(sm.poison_in() + w));
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the ring reads stay after the count
         const double* blk = lin + hslot(c0 + 1);  // entries c0 + 1 .. c0 + U - 1
         dst[0] = lin[hslot(c0)];
         const double2* src = reinterpret_cast<const double2*>(blk);
@@ -841,15 +858,13 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         constexpr bool INTERIOR = decltype(interior_tag)::value;
 #pragma unroll
         for (int u = 0; u < U; ++u) d_cur[u] = d_nxt[u];
-        if (!cost.begin(cring, s0 + 2 * TC) || !fetch_lds(s0, up_cur)) return -1;
+        int pz, bc;
+        if (!cost.begin(cring, s0 + 2 * TC) || !fetch_lds(s0, up_cur, pz, bc)) return -1;
         if constexpr (FINITE) {
             // the group's costs reach column s0 + U - 1; the band above's entries come from a
             // band that has left the finite-input cell, or (across workgroups) were seen
-            // non-finite by the helper wave: both flags are stored before the counts this
-            // group has waited for
-            bool bad = cost.first_bad_col() <= s0 + U - 1;
-            if (b > 0) bad = bad || __builtin_amdgcn_readfirstlane(lds_load(sm.poison_in() + w)) != 0;
-            if (bad) return 1;
+            // non-finite by the helper wave
+            if (bc <= s0 + U - 1 || (b > 0 && pz != 0)) return 1;
         }
         // this group writes columns up to s0 + U - 64 of my last row; writing column c
         // reuses the slot of column c - RS, which the consumer must have taken
