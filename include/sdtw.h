@@ -141,7 +141,8 @@ int sdtw_sqeuclid_fwd_f32(const float *x, const float *y, float *D, int64_t B, i
  *   G' = G where (x2 + y2 - 2xy) >= 0 else 0            (clamp_min backward)
  *   gx = 2 (x * rowsum(G') - G' y),  gy = 2 (y * colsum(G') - G'^T x)
  * D is the clamped forward output (used to find clamped cells).  mask = 0 skips the clamp
- * mask (the fused-mode chain rule of autograd_xy.py:45-49 has none).
+ * mask (the fused-mode chain rule of autograd_xy.py:45-49 has none).  gx or gy may be NULL:
+ * that gradient is not formed (autograd's needs_input_grad); both NULL is a no-op.
  * Replaces the torch autograd backward of distances.py:20-28 (bmm/sum/clamp_min
  * backward) and, with mask = 0, autograd_xy.py:41-49. */
 int sdtw_sqeuclid_bwd_f32(const float *x, const float *y, const float *D, const float *G,
@@ -196,7 +197,8 @@ int sdtw_fused_fwd_d_f32(const float *x, const float *y, float *D, float *R, flo
 
 /* Fused backward: E recomputed with per-cell costs from x, y, then
  *   gx = 2 (x * rowsum(gE) - gE y),  gy = 2 (y * colsum(gE) - gE^T x),  gE = gout[b] * E.
- * gout may be NULL (treated as 1).  E lives only in the workspace.
+ * gout may be NULL (treated as 1).  E lives only in the workspace.  gx or gy may be NULL:
+ * that gradient is not formed; both NULL is a no-op.
  * Replaces softdtw_cuda/cuda/launcher.py:90-162 (softdtw_backward_cuda_fused_sqeuclid)
  * together with the chain rule of autograd_xy.py:32-51. */
 int sdtw_fused_bwd_f32(const float *x, const float *y, const float *R, const float *gout,
@@ -209,6 +211,26 @@ int sdtw_fused_bwd_f32(const float *x, const float *y, const float *R, const flo
 int sdtw_fused_bwd_e_f32(const float *x, const float *y, const float *R, const float *gout,
                          float *E, int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
                          double bandwidth, void *ws, size_t ws_bytes, void *stream);
+
+/* ---- barycenter ----------------------------------------------------------------------------
+ * softdtw_barycenter (barycenters.py:17-180) with its loop on the device: per iteration the
+ * fused forward of the barycenter (N, K) broadcast to every pair against X (B, N, K), the
+ * fused backward with upstream gradient w (so no gradient of X is formed), then one update
+ * kernel: the gradient summed over pairs, clipped to norm 1 (clip_grad_norm_), torch's Adam
+ * step (betas 0.9 / 0.999, eps 1e-8) with learning rate lrs[it] (the caller passes the
+ * schedule's values, e.g. torch's CosineAnnealingLR), and the weighted loss sum_b w_b out_b of
+ * the iterate before the step.  w are the normalised weights (device, B); bary holds the
+ * initial barycenter and receives the result; losses (device, max_iter, or NULL) receives
+ * the loss of each iteration run; *iters_run the number of iterations run.
+ * early_stopping != 0 applies the reference's rule (stop once `patience` iterations in a row
+ * improved the loss by no more than tol, after max_iter / 2): each iteration then copies its
+ * loss to the host and synchronises the stream -- the only entry point besides
+ * sdtw_debug_status that synchronises.  Workspace: sdtw_barycenter_workspace_bytes. */
+size_t sdtw_barycenter_workspace_bytes(int64_t B, int64_t N, int64_t K, int max_iter);
+int sdtw_barycenter_f32(const float *X, const float *w, float *bary, float *losses, int64_t B,
+                        int64_t N, int64_t K, double gamma, int max_iter, const double *lrs,
+                        int early_stopping, int patience, double tol, int *iters_run, void *ws,
+                        size_t ws_bytes, void *stream);
 
 /* ---- float64 path ------------------------------------------------------------------------
  * The reference keeps the caller's dtype: float64 inputs give a float64 cost

@@ -303,8 +303,8 @@ int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const 
                           float* gx, float* gy, int64_t B, int64_t N, int64_t M, int64_t K,
                           int mask, void* ws, size_t ws_bytes, void* stream) {
     if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
-    if (B == 0) return SDTW_OK;
-    if (!x || !y || !G || !gx || !gy || (mask && !D)) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0 || (!gx && !gy)) return SDTW_OK;
+    if (!x || !y || !G || (mask && !D)) return SDTW_ERR_INVALID_VALUE;
     if (!dist_grid_ok(B, N, M)) return SDTW_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
     DistBwdParams p{};
@@ -459,8 +459,8 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
                        double gamma, double bandwidth, void* ws, size_t ws_bytes,
                        void* stream) {
     if (!shape_ok(B, N, M, K, true) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
-    if (B == 0) return SDTW_OK;
-    if (!x || !y || !R || !gx || !gy) return SDTW_ERR_INVALID_VALUE;
+    if (B == 0 || (!gx && !gy)) return SDTW_OK;
+    if (!x || !y || !R) return SDTW_ERR_INVALID_VALUE;
     if (!dist_grid_ok(B, N, M)) return SDTW_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
     Carver c{static_cast<char*>(ws), ws_bytes};
@@ -504,6 +504,97 @@ int sdtw_fused_bwd_e_f32(const float* x, const float* y, const float* R, const f
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     return fused_bwd_common(x, y, R, gout, E, x2, y2, d, B, N, M, K, gamma, bandwidth,
                             (hipStream_t)stream);
+}
+
+// Barycenter loop: [xb (B,N,K)][out (B)][gx (B,N,K)][m, v, grad (N,K) each][losses][R]
+// [recursion workspace, the larger of the fused forward's and backward's]
+static size_t bary_rec_bytes(int64_t B, int64_t N, int64_t K) {
+    const size_t f = sdtw_workspace_bytes(SDTW_OP_FUSED_FWD, B, N, N, K);
+    const size_t g = sdtw_workspace_bytes(SDTW_OP_FUSED_BWD, B, N, N, K);
+    return f > g ? f : g;
+}
+
+size_t sdtw_barycenter_workspace_bytes(int64_t B, int64_t N, int64_t K, int max_iter) {
+    if (!shape_ok(B, N, N, K, true) || B == 0 || max_iter < 0) return 0;
+    const int64_t nk = N * K;
+    return 2 * align_up(sizeof(float) * B * nk) + align_up(sizeof(float) * B) +
+           3 * align_up(sizeof(float) * nk) + align_up(sizeof(float) * (max_iter > 0 ? max_iter : 1)) +
+           align_up(sizeof(float) * dp_table_elems(B, N, N)) + bary_rec_bytes(B, N, K);
+}
+
+int sdtw_barycenter_f32(const float* X, const float* w, float* bary, float* losses,
+                        int64_t B, int64_t N, int64_t K, double gamma, int max_iter,
+                        const double* lrs, int early_stopping, int patience, double tol,
+                        int* iters_run, void* ws, size_t ws_bytes, void* stream) {
+    if (!shape_ok(B, N, N, K, true) || B == 0 || !gamma_ok(gamma) || max_iter < 0)
+        return SDTW_ERR_INVALID_VALUE;
+    if (!X || !w || !bary || (max_iter > 0 && !lrs)) return SDTW_ERR_INVALID_VALUE;
+    if (!dist_grid_ok(B, N, N)) return SDTW_ERR_UNSUPPORTED;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nk = N * K;
+    Carver c{static_cast<char*>(ws), ws_bytes};
+    float* xb = c.take<float>(B * nk);
+    float* out = c.take<float>(B);
+    float* gx = c.take<float>(B * nk);
+    float* m = c.take<float>(nk);
+    float* v = c.take<float>(nk);
+    float* gbuf = c.take<float>(nk);
+    float* loss = c.take<float>(max_iter > 0 ? max_iter : 1);
+    float* R = c.take<float>(dp_table_elems(B, N, N));
+    const size_t rec_bytes = bary_rec_bytes(B, N, K);
+    void* rec = c.take<unsigned char>(rec_bytes);
+    if (!c.ok) return SDTW_ERR_WORKSPACE;
+    if (launch_fill_zero(m, nk, st) != hipSuccess || launch_fill_zero(v, nk, st) != hipSuccess)
+        return SDTW_ERR_LAUNCH;
+    double best = INFINITY;
+    int wait = 0, it = 0;
+    for (; it < max_iter; ++it) {
+        // losses of the barycenter against every sequence, and d loss / d barycenter per pair
+        // (the backward's upstream gradient is the weights; dL/dX is not formed)
+        if (launch_bary_broadcast(bary, xb, B, nk, st) != hipSuccess) return SDTW_ERR_LAUNCH;
+        int rc = fused_fwd_common(xb, X, nullptr, R, out, B, N, N, K, gamma, -1.0, rec, rec_bytes,
+                                  stream);
+        if (rc != SDTW_OK) return rc;
+        rc = sdtw_fused_bwd_f32(xb, X, R, w, gx, nullptr, B, N, N, K, gamma, -1.0, rec, rec_bytes,
+                                stream);
+        if (rc != SDTW_OK) return rc;
+        // Adam step t = it + 1 with the scalars torch's Adam forms in double
+        const double t = (double)(it + 1);
+        const double bc1 = 1.0 - pow(0.9, t), bc2 = 1.0 - pow(0.999, t);
+        BaryStep s;
+        s.one_m_b1 = (float)(1.0 - 0.9);
+        s.b2 = (float)0.999;
+        s.one_m_b2 = (float)(1.0 - 0.999);
+        s.bc2_sqrt = (float)pow(bc2, 0.5);
+        s.eps = (float)1e-8;
+        s.neg_step = (float)(lrs[it] / bc1 * -1.0);
+        s.max_norm = 1.0f;
+        if (launch_bary_update(gx, out, w, bary, m, v, gbuf, loss + it, (int)B, (int)nk, s, st) !=
+            hipSuccess)
+            return SDTW_ERR_LAUNCH;
+        if (early_stopping) {  // the reference's rule (barycenters.py:149-165) needs the loss
+            float lv = 0.0f;
+            if (hipMemcpyAsync(&lv, loss + it, sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess ||
+                hipStreamSynchronize(st) != hipSuccess)
+                return SDTW_ERR_LAUNCH;
+            const double improvement = best - (double)lv;
+            if (improvement > tol) {
+                best = lv;
+                wait = 0;
+            } else {
+                ++wait;
+            }
+            if (wait >= patience && it > max_iter / 2) {
+                ++it;
+                break;
+            }
+        }
+    }
+    if (iters_run) *iters_run = it;
+    if (losses && it > 0 &&
+        hipMemcpyAsync(losses, loss, sizeof(float) * it, hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return SDTW_ERR_LAUNCH;
+    return SDTW_OK;
 }
 
 }  // extern "C"

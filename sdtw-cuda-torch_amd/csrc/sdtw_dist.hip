@@ -763,16 +763,17 @@ hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st) {
         const int blocks = (int)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
         hipLaunchKernelGGL(zero_ints_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, st, p.cnt, n);
     }
-    // with the mask, the gx pass writes one flag per workgroup, which the gy pass reads
+    // with the mask, the gx pass writes one flag per workgroup, which the gy pass reads; a
+    // null gx or gy skips that pass (a gy pass without a gx pass applies the full mask)
     DistBwdParams q = p;
-    if (!q.mask) q.flags = nullptr;
+    if (!q.mask || !q.gx) q.flags = nullptr;
     q.nflags = (int)(dist_bwd_tiles(p.B, p.N, p.K) * (p.part ? dist_bwd_splits(p.B, p.N, p.M, p.K) : 1));
     if (q.muladd) {
-        launch_dist_bwd_one<false, true>(q, st);
-        launch_dist_bwd_one<true, true>(q, st);
+        if (q.gx) launch_dist_bwd_one<false, true>(q, st);
+        if (q.gy) launch_dist_bwd_one<true, true>(q, st);
     } else {
-        launch_dist_bwd_one<false, false>(q, st);
-        launch_dist_bwd_one<true, false>(q, st);
+        if (q.gx) launch_dist_bwd_one<false, false>(q, st);
+        if (q.gy) launch_dist_bwd_one<true, false>(q, st);
     }
     return hipGetLastError();
 }

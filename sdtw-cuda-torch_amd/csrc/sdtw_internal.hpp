@@ -120,6 +120,24 @@ hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st);
 hipError_t launch_fwd(const DPParams& p, bool fused, bool muladd, bool exact, hipStream_t st);
 hipError_t launch_bwd(const DPParams& p, bool fused, bool muladd, bool exact, hipStream_t st);
 hipError_t launch_table_unpack(const float* Rt, float* Rd, int B, int N, int M, hipStream_t st);
+
+// One barycenter update (sdtw_bary.hip): scalars of the Adam step and the clip, fp32 as the
+// element-wise optimiser arithmetic uses them.
+struct BaryStep {
+    float one_m_b1;  // 1 - beta1
+    float b2;        // beta2
+    float one_m_b2;  // 1 - beta2
+    float bc2_sqrt;  // sqrt(1 - beta2^t)
+    float eps;
+    float neg_step;  // -lr / (1 - beta1^t)
+    float max_norm;  // gradient-norm clip
+};
+hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
+hipError_t launch_bary_broadcast(const float* bary, float* xb, int64_t B, int64_t NK,
+                                 hipStream_t st);
+hipError_t launch_bary_update(const float* gx, const float* out, const float* w, float* bary,
+                              float* m, float* v, float* gbuf, float* loss, int B, int NK,
+                              const BaryStep& s, hipStream_t st);
 hipError_t launch_table_pack(const float* Rd, float* Rt, int B, int N, int M, hipStream_t st);
 
 // Geometry of the band decomposition used by the wavefront kernels.

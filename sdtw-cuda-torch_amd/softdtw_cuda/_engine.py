@@ -64,6 +64,11 @@ _SIGS = {
     "sdtw_fused_bwd_e_f32": ([ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4
                              + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                              ctypes.c_int),
+    "sdtw_barycenter_workspace_bytes": ([ctypes.c_int64] * 3 + [ctypes.c_int], ctypes.c_size_t),
+    "sdtw_barycenter_f32": ([ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3
+                            + [ctypes.c_double, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                               ctypes.c_int, ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p,
+                               ctypes.c_size_t, ctypes.c_void_p], ctypes.c_int),
     "sdtw_table_elems_f64": ([ctypes.c_int64] * 3, ctypes.c_int64),
     "sdtw_sqeuclid_fwd_f64": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4 + [ctypes.c_void_p],
                               ctypes.c_int),
@@ -246,7 +251,9 @@ def sqeuclid_fwd(x: torch.Tensor, y: torch.Tensor, mode: int = DIST_EXACT) -> to
     return D
 
 
-def sqeuclid_bwd(x, y, D, G, mask: bool = True):
+def sqeuclid_bwd(x, y, D, G, mask: bool = True, need=(True, True)):
+    """(gx, gy) of the distance given G = dL/dD; an entry of `need` that is False skips that
+    gradient (returned as None)."""
     for t, n in ((x, "x"), (y, "y"), (G, "G")):
         require_gpu(t, f"sqeuclid backward {n}")
     if mask:
@@ -256,8 +263,8 @@ def sqeuclid_bwd(x, y, D, G, mask: bool = True):
         _check_shapes(x=x, y=y, D=D)
     B, N, K = x.shape
     M = y.shape[1]
-    gx = torch.empty_like(x)
-    gy = torch.empty_like(y)
+    gx = torch.empty_like(x) if need[0] else None
+    gy = torch.empty_like(y) if need[1] else None
     ws, nws = _workspace(OP_SQEUCLID_BWD, B, N, M, K, x.device)
     with torch.cuda.device(x.device):
         rc = load().sdtw_sqeuclid_bwd_f32(_ptr(x), _ptr(y), _ptr(D if mask else None), _ptr(G),
@@ -384,7 +391,9 @@ def fused_fwd_d(x, y, gamma: float, bandwidth: float):
     return out, R, D
 
 
-def fused_bwd(x, y, R, gamma: float, bandwidth: float, gout=None):
+def fused_bwd(x, y, R, gamma: float, bandwidth: float, gout=None, need=(True, True)):
+    """(gx, gy) of the fused Soft-DTW; an entry of `need` that is False skips that gradient
+    (returned as None)."""
     require_gpu(x, "fused backward x")
     require_gpu(y, "fused backward y")
     require_gpu(R, "fused backward R")
@@ -393,8 +402,8 @@ def fused_bwd(x, y, R, gamma: float, bandwidth: float, gout=None):
     _check_shapes(x=x, y=y, R=R, gout=gout)
     B, N, K = x.shape
     M = y.shape[1]
-    gx = torch.empty_like(x)
-    gy = torch.empty_like(y)
+    gx = torch.empty_like(x) if need[0] else None
+    gy = torch.empty_like(y) if need[1] else None
     ws, nws = _workspace(OP_FUSED_BWD, B, N, M, K, x.device)
     with torch.cuda.device(x.device):
         rc = load().sdtw_fused_bwd_f32(_ptr(x), _ptr(y), _ptr(R), _ptr(gout), _ptr(gx), _ptr(gy),
@@ -423,6 +432,30 @@ def fused_bwd_e(x, y, R, gamma: float, bandwidth: float, gout=None):
     _check(rc, "fused backward (E)")
     _debug_check(OP_FUSED_BWD, ws, nws, B, N, M, K, "fused backward (E)")
     return E
+
+
+def barycenter(X, w, bary, gamma: float, lrs, early_stopping: bool, patience: int, tol: float):
+    """sdtw_barycenter_f32: the barycenter loop on the device.  X (B, N, K) sequences, w (B,)
+    normalised weights, bary (N, K) the initial barycenter, updated in place; lrs the
+    learning rate of each iteration.  Returns (bary, losses of the iterations run)."""
+    for t, n in ((X, "X"), (w, "weights"), (bary, "barycenter")):
+        require_gpu(t, f"barycenter {n}")
+    if X.dim() != 3 or tuple(bary.shape) != tuple(X.shape[1:]) or w.numel() != X.shape[0]:
+        raise ValueError("softdtw_cuda: barycenter expects X (B,N,K), weights (B,), init (N,K)")
+    B, N, K = X.shape
+    max_iter = len(lrs)
+    n = int(load().sdtw_barycenter_workspace_bytes(B, N, K, max_iter))
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device=X.device)
+    losses = torch.empty(max(max_iter, 1), dtype=torch.float32, device=X.device)
+    lr_arr = (ctypes.c_double * max(max_iter, 1))(*lrs)
+    iters = ctypes.c_int(0)
+    with torch.cuda.device(X.device):
+        rc = load().sdtw_barycenter_f32(_ptr(X), _ptr(w), _ptr(bary), _ptr(losses), B, N, K,
+                                        float(gamma), max_iter, lr_arr, 1 if early_stopping else 0,
+                                        int(patience), float(tol), ctypes.byref(iters), _ptr(ws), n,
+                                        _stream(X.device))
+    _check(rc, "barycenter")
+    return bary, losses[:iters.value]
 
 
 # ---- float64 path (sdtw_*_f64): double throughout, R the dense (B, N+2, M+2) table -------

@@ -77,6 +77,5 @@ class SoftDTWSqEuclidAutograd(Function):
         x, y, D, R = ctx.saved_tensors
         g = grad_output.reshape(-1).to(device=D.device, dtype=torch.float32).contiguous()
         G = _engine.dtw_bwd(D, R, ctx.gamma, ctx.bandwidth, gout=g)
-        gx, gy = _engine.sqeuclid_bwd(x, y, D, G, mask=True)
-        return (gx if ctx.needs_input_grad[0] else None,
-                gy if ctx.needs_input_grad[1] else None, None, None)
+        gx, gy = _engine.sqeuclid_bwd(x, y, D, G, mask=True, need=ctx.needs_input_grad[:2])
+        return gx, gy, None, None

@@ -51,11 +51,14 @@ class SoftDTWXYAutograd(Function):
     def backward(ctx, grad_output: torch.Tensor):
         Xg, Yg, R = ctx.saved_tensors[:3]
         g = grad_output.reshape(-1).to(device=Xg.device, dtype=Xg.dtype).contiguous()
+        need = ctx.needs_input_grad[:2]
         if Xg.dtype == torch.float64:
             D = ctx.saved_tensors[3]
             G = _engine.dtw_bwd64(D, R, ctx.gamma, ctx.bandwidth, gout=g)
             gx, gy = _engine.sqeuclid_bwd64(Xg, Yg, None, G, mask=False)
         else:
-            gx, gy = _engine.fused_bwd(Xg, Yg, R, ctx.gamma, ctx.bandwidth, gout=g)
+            # only the gradients autograd asks for (a barycenter's sequences need none)
+            gx, gy = _engine.fused_bwd(Xg, Yg, R, ctx.gamma, ctx.bandwidth, gout=g, need=need)
         dx, dy = ctx.dtypes
-        return gx.to(dtype=dx), gy.to(dtype=dy), None, None
+        return (gx.to(dtype=dx) if need[0] else None, gy.to(dtype=dy) if need[1] else None,
+                None, None)

@@ -12,7 +12,30 @@ import time
 
 import torch
 
+from . import _engine
 from .module import SoftDTW
+
+
+def _cosine_lrs(lr: float, max_iter: int) -> list[float]:
+    """The learning rate of each iteration: Adam(lr) under CosineAnnealingLR(T_max=max_iter,
+    eta_min=0.1 lr), read off torch's own scheduler (barycenters.py:101-106)."""
+    p = torch.zeros(1, requires_grad=True)
+    opt = torch.optim.Adam([p], lr=lr)
+    sched = torch.optim.lr_scheduler.CosineAnnealingLR(opt, T_max=max_iter, eta_min=lr * 0.1)
+    out = []
+    for _ in range(max_iter):
+        out.append(float(opt.param_groups[0]["lr"]))
+        opt.step()  # no gradient: nothing changes, but the scheduler sees a step first
+        sched.step()
+    return out
+
+
+def _device_loop_applies(X, barycenter, weights, fused, verbose) -> bool:
+    """The device loop (sdtw_barycenter_f32) runs the reference's GPU default: float32 CUDA
+    tensors, the fused Soft-DTW, no progress printing."""
+    return (X.is_cuda and X.dtype == torch.float32 and barycenter.dtype == torch.float32
+            and weights.dtype == torch.float32 and fused in (None, True) and not verbose
+            and X.dim() == 3 and X.shape[0] > 0)
 
 
 def softdtw_barycenter(
@@ -52,6 +75,16 @@ def softdtw_barycenter(
         barycenter = (X * weights.view(B, 1, 1)).sum(dim=0).clone()
     else:
         barycenter = init.clone().to(device)
+
+    if _device_loop_applies(X, barycenter, weights, fused, verbose):
+        # the whole loop on the device: the recursions on the fused kernels, the gradient sum,
+        # clipping and Adam step in one kernel per iteration, the learning rates from torch's
+        # own scheduler
+        bary, _ = _engine.barycenter(X.contiguous(), weights.contiguous(), barycenter.contiguous(),
+                                     gamma, _cosine_lrs(lr, max_iter), early_stopping, patience,
+                                     tol)
+        return bary
+
     barycenter = barycenter.requires_grad_(True)
 
     loss_fn = SoftDTW(gamma=gamma, normalize=False, fused=fused)

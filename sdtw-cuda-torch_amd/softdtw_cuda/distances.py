@@ -21,9 +21,9 @@ class _SqEuclideanHIP(Function):
     @staticmethod
     def backward(ctx, G):
         x, y, D = ctx.saved_tensors
-        gx, gy = _engine.sqeuclid_bwd(x, y, D, G.contiguous().to(torch.float32), mask=True)
-        return (gx if ctx.needs_input_grad[0] else None,
-                gy if ctx.needs_input_grad[1] else None)
+        gx, gy = _engine.sqeuclid_bwd(x, y, D, G.contiguous().to(torch.float32), mask=True,
+                                      need=ctx.needs_input_grad[:2])
+        return gx, gy
 
 
 class _SqEuclideanHIP64(Function):
