@@ -506,8 +506,8 @@ int sdtw_fused_bwd_e_f32(const float* x, const float* y, const float* R, const f
                             (hipStream_t)stream);
 }
 
-// Barycenter loop: [xb (B,N,K)][out (B)][gx (B,N,K)][m, v, grad (N,K) each][losses][R]
-// [recursion workspace, the larger of the fused forward's and backward's]
+// Barycenter loop: [xb (B,N,K)][out (B)][gx (B,N,K)][m, v, grad (N,K) each][norm partials]
+// [losses][R][recursion workspace, the larger of the fused forward's and backward's]
 static size_t bary_rec_bytes(int64_t B, int64_t N, int64_t K) {
     const size_t f = sdtw_workspace_bytes(SDTW_OP_FUSED_FWD, B, N, N, K);
     const size_t g = sdtw_workspace_bytes(SDTW_OP_FUSED_BWD, B, N, N, K);
@@ -518,7 +518,8 @@ size_t sdtw_barycenter_workspace_bytes(int64_t B, int64_t N, int64_t K, int max_
     if (!shape_ok(B, N, N, K, true) || B == 0 || max_iter < 0) return 0;
     const int64_t nk = N * K;
     return 2 * align_up(sizeof(float) * B * nk) + align_up(sizeof(float) * B) +
-           3 * align_up(sizeof(float) * nk) + align_up(sizeof(float) * (max_iter > 0 ? max_iter : 1)) +
+           3 * align_up(sizeof(float) * nk) + align_up(sizeof(float) * bary_parts(nk)) +
+           align_up(sizeof(float) * (max_iter > 0 ? max_iter : 1)) +
            align_up(sizeof(float) * dp_table_elems(B, N, N)) + bary_rec_bytes(B, N, K);
 }
 
@@ -539,19 +540,21 @@ int sdtw_barycenter_f32(const float* X, const float* w, float* bary, float* loss
     float* m = c.take<float>(nk);
     float* v = c.take<float>(nk);
     float* gbuf = c.take<float>(nk);
+    float* part = c.take<float>(bary_parts(nk));
     float* loss = c.take<float>(max_iter > 0 ? max_iter : 1);
     float* R = c.take<float>(dp_table_elems(B, N, N));
     const size_t rec_bytes = bary_rec_bytes(B, N, K);
     void* rec = c.take<unsigned char>(rec_bytes);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
-    if (launch_fill_zero(m, nk, st) != hipSuccess || launch_fill_zero(v, nk, st) != hipSuccess)
+    if (launch_fill_zero(m, nk, st) != hipSuccess || launch_fill_zero(v, nk, st) != hipSuccess ||
+        launch_bary_broadcast(bary, xb, B, nk, st) != hipSuccess)
         return SDTW_ERR_LAUNCH;
     double best = INFINITY;
     int wait = 0, it = 0;
     for (; it < max_iter; ++it) {
-        // losses of the barycenter against every sequence, and d loss / d barycenter per pair
-        // (the backward's upstream gradient is the weights; dL/dX is not formed)
-        if (launch_bary_broadcast(bary, xb, B, nk, st) != hipSuccess) return SDTW_ERR_LAUNCH;
+        // losses of the barycenter (xb: its copy per pair) against every sequence, and
+        // d loss / d barycenter per pair (the backward's upstream gradient is the weights;
+        // dL/dX is not formed)
         int rc = fused_fwd_common(xb, X, nullptr, R, out, B, N, N, K, gamma, -1.0, rec, rec_bytes,
                                   stream);
         if (rc != SDTW_OK) return rc;
@@ -569,8 +572,8 @@ int sdtw_barycenter_f32(const float* X, const float* w, float* bary, float* loss
         s.eps = (float)1e-8;
         s.neg_step = (float)(lrs[it] / bc1 * -1.0);
         s.max_norm = 1.0f;
-        if (launch_bary_update(gx, out, w, bary, m, v, gbuf, loss + it, (int)B, (int)nk, s, st) !=
-            hipSuccess)
+        if (launch_bary_update(gx, out, w, bary, xb, m, v, gbuf, part, loss + it, (int)B, (int)nk,
+                               s, st) != hipSuccess)
             return SDTW_ERR_LAUNCH;
         if (early_stopping) {  // the reference's rule (barycenters.py:149-165) needs the loss
             float lv = 0.0f;

@@ -135,9 +135,13 @@ struct BaryStep {
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 hipError_t launch_bary_broadcast(const float* bary, float* xb, int64_t B, int64_t NK,
                                  hipStream_t st);
+// Workgroups of the gradient reduction (the number of partial sums it leaves in `part`).
+int bary_parts(int64_t NK);
+// The clipped Adam step of the barycenter from the per-pair gradients gx (B, NK); also
+// writes the new barycenter into every pair's copy xb (B, NK) and the weighted loss.
 hipError_t launch_bary_update(const float* gx, const float* out, const float* w, float* bary,
-                              float* m, float* v, float* gbuf, float* loss, int B, int NK,
-                              const BaryStep& s, hipStream_t st);
+                              float* xb, float* m, float* v, float* gbuf, float* part,
+                              float* loss, int B, int NK, const BaryStep& s, hipStream_t st);
 hipError_t launch_table_pack(const float* Rd, float* Rt, int B, int N, int M, hipStream_t st);
 
 // Geometry of the band decomposition used by the wavefront kernels.
