@@ -22,7 +22,9 @@
  *     contiguous floats).  Its cells are the reference's R[b,i+1,j+1] (launcher.py:177)
  *     rounded once from an fp64 recursion; out-of-band cells hold +inf.  Convert with
  *     sdtw_table_unpack_f32 / sdtw_table_pack_f32.
- *   - Re-entrant and stateless apart from a once-only device-attribute query.
+ *   - Re-entrant.  The only state: the process-wide settings (sdtw_set_numerics,
+ *     sdtw_set_wait_limit, sdtw_set_deterministic), the no-allocation entry point's static
+ *     scratch, and a once-only device-attribute query.
  */
 #ifndef SDTW_H_
 #define SDTW_H_
@@ -98,7 +100,9 @@ int sdtw_get_numerics(void);
  * `op` that used workspace `ws` hit its bounded inter-band wait, else SDTW_OK.  The kernels
  * never hang: a wait that expires raises this flag, the wave stops, and the pair's results
  * are marked invalid without any synchronisation -- out[p] = NaN (forward), NaN over the
- * band's rows of G or E (backward), and so NaN gradients through the distance backward.
+ * band's rows of G or E (backward), and so NaN gradients through the distance backward; in
+ * the fused backward's gradient mode, NaN over the band's rows of dL/dx and all of the
+ * pair's dL/dy.
  * No counterpart in the reference (whose kernels have no inter-block waits). */
 int sdtw_debug_status(int op, const void *ws, size_t ws_bytes, int64_t B, int64_t N, int64_t M,
                       int64_t K);
@@ -109,6 +113,15 @@ int sdtw_debug_status(int op, const void *ws, size_t ws_bytes, int64_t B, int64_
  * once (every kernel still exits normally), so the give-up path can be exercised.  No
  * counterpart in the reference. */
 unsigned sdtw_set_wait_limit(unsigned polls);
+
+/* Process-wide: 1 makes sdtw_fused_bwd_f32 give run-to-run identical bits by taking its
+ * E path (g*E in the workspace, reduced by the distance backward); 0 (the default) lets it
+ * form the gradients inside the recursion kernel, whose dL/dy adds the bands' shares with
+ * atomics in arrival order (last-bit differences between runs).  Takes effect for calls
+ * (and sdtw_workspace_bytes queries) made after it.  Returns the previous setting.  No
+ * counterpart in the reference; the torch layer sets it from
+ * torch.are_deterministic_algorithms_enabled(). */
+int sdtw_set_deterministic(int on);
 
 /* Bands per workgroup the fused recursions (sdtw_fused_fwd_f32, sdtw_fused_fwd_d_f32,
  * sdtw_fused_bwd_f32) take at this shape on the current device: 2 when the batch's 2-band
@@ -197,8 +210,13 @@ int sdtw_fused_fwd_d_f32(const float *x, const float *y, float *D, float *R, flo
 
 /* Fused backward: E recomputed with per-cell costs from x, y, then
  *   gx = 2 (x * rowsum(gE) - gE y),  gy = 2 (y * colsum(gE) - gE^T x),  gE = gout[b] * E.
- * gout may be NULL (treated as 1).  E lives only in the workspace.  gx or gy may be NULL:
- * that gradient is not formed; both NULL is a no-op.
+ * gout may be NULL (treated as 1).  gx or gy may be NULL: that gradient is not formed; both
+ * NULL is a no-op.  With matrix-core cost tiles (K <= 64, K*N*M >= 400) in workgroups of at
+ * most 2 bands, or 4 when K <= 16, the recursion kernel forms gx and gy from E tile by tile
+ * and nothing of size (B,N,M) exists; gy then adds the bands' shares with atomics in
+ * arrival order (see sdtw_set_deterministic).  Otherwise, and under the deterministic
+ * setting, E lives in the workspace and the distance backward reduces it.
+ * sdtw_workspace_bytes(SDTW_OP_FUSED_BWD, ...) sizes the path taken.
  * Replaces softdtw_cuda/cuda/launcher.py:90-162 (softdtw_backward_cuda_fused_sqeuclid)
  * together with the chain rule of autograd_xy.py:32-51. */
 int sdtw_fused_bwd_f32(const float *x, const float *y, const float *R, const float *gout,

@@ -91,6 +91,21 @@ int fused_wmax(int64_t B, int64_t N, int64_t M, int64_t K) {
 }
 // workspace sizing: the 2-band geometry needs the most cross-workgroup rows
 int fused_ws_wmax(int64_t N, int64_t M, int64_t K) { return mfma_costs(N, M, K) ? 2 : 4; }
+// Process-wide: whether the fused backward must give run-to-run identical bits
+// (sdtw_set_deterministic).
+std::atomic<int> g_deterministic{0};
+// The fused backward forms dL/dx and dL/dy inside the recursion kernel (gradient mode,
+// no (B,N,M) buffer) with matrix-core cost tiles in a geometry whose waves fit: workgroups
+// of up to 2 bands, or up to 4 for K <= 16.  Its dL/dy sums the bands' shares in arrival
+// order, so under the deterministic setting a call that forms dL/dy, like every other call,
+// writes g*E and reduces it with the distance backward (dL/dx alone is formed in a fixed
+// order either way).  Workspace queries assume dL/dy is formed: the E path's workspace
+// holds the gradient mode's.
+bool fused_grad_mode(int64_t B, int64_t N, int64_t M, int64_t K, bool forms_gy = true) {
+    if (forms_gy && g_deterministic.load(std::memory_order_relaxed)) return false;
+    if (!mfma_costs(N, M, K)) return false;
+    return fused_wmax(B, N, M, K) <= 2 || K <= 16;
+}
 
 // distance-backward split-reduction scratch: partials, then counters
 size_t ws_dist_bwd(int64_t B, int64_t N, int64_t M, int64_t K) {
@@ -210,6 +225,8 @@ int sdtw_get_numerics(void) { return g_numerics.load(); }
 
 unsigned sdtw_set_wait_limit(unsigned polls) { return g_spin_limit.exchange(polls); }
 
+int sdtw_set_deterministic(int on) { return g_deterministic.exchange(on ? 1 : 0); }
+
 int sdtw_fused_bands_per_workgroup(int64_t B, int64_t N, int64_t M, int64_t K) {
     if (!shape_ok(B, N, M, K, true)) return 0;
     return fused_wmax(B, N, M, K);
@@ -271,6 +288,8 @@ size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) 
         case SDTW_OP_FUSED_FWD:
             return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(N, M, K));
         case SDTW_OP_FUSED_BWD:
+            if (fused_grad_mode(B, N, M, K))
+                return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(N, M, K));
             return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(N, M, K)) + align_up(sizeof(float) * B * N * M) +
                    ws_dist_bwd(B, N, M, K);
         default:
@@ -461,12 +480,30 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
     if (!shape_ok(B, N, M, K, true) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
     if (B == 0 || (!gx && !gy)) return SDTW_OK;
     if (!x || !y || !R) return SDTW_ERR_INVALID_VALUE;
-    if (!dist_grid_ok(B, N, M)) return SDTW_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
     const DPScratch d = carve_dp(c, B, N, M, fused_wmax(B, N, M, K));
+    if (fused_grad_mode(B, N, M, K, gy != nullptr)) {
+        // the gradients inside the recursion kernel: dL/dy is zeroed by the prep launch and
+        // accumulated band by band, dL/dx written per band
+        if (!c.ok) return SDTW_ERR_WORKSPACE;
+        DPParams p{};
+        fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_wmax(B, N, M, K));
+        p.x = x;
+        p.y = y;
+        p.x2 = x2;
+        p.y2 = y2;
+        p.x2_fill = x2;
+        p.y2_fill = y2;
+        p.R = const_cast<float*>(R);
+        p.gout = gout;
+        p.gx_out = gx;
+        p.gy_out = gy;
+        return status_of(launch_bwd(p, true, false, exact_backward(), st));
+    }
+    if (!dist_grid_ok(B, N, M)) return SDTW_ERR_UNSUPPORTED;
     float* Ebuf = c.take<float>(B * N * M);
     float* part = c.take<float>(dist_bwd_split_floats(B, N, M, K));
     int* cnt = c.take<int>(dist_bwd_counters(B, N, M, K));

@@ -67,11 +67,13 @@ __global__ void __launch_bounds__(256) norms_kernel(const float* __restrict__ v0
     norms_at((int64_t)blockIdx.x * blockDim.x + threadIdx.x, v0, out0, rows0, v1, out1, rows1, K);
 }
 
-// Blocks [0, prep_blocks) do the wavefront launch's prep work, the rest the norms (each block
-// takes one job whole, so the norms' shuffles stay within full waves).
+// Blocks [0, prep_blocks) do the wavefront launch's prep work, the next zero_blocks zero the
+// word ranges z0 and z1, the rest form the norms (each block takes one job whole, so the
+// norms' shuffles stay within full waves).
 __global__ void __launch_bounds__(256) prep_norms_kernel(
     int* ticket, int* err, unsigned long long* rows, int64_t nwords, unsigned long long lo,
-    unsigned long long hi, int prep_blocks, const float* __restrict__ v0,
+    unsigned long long hi, int prep_blocks, int zero_blocks, unsigned* __restrict__ z0,
+    int64_t n0, unsigned* __restrict__ z1, int64_t n1, const float* __restrict__ v0,
     float* __restrict__ out0, int64_t rows0, const float* __restrict__ v1,
     float* __restrict__ out1, int64_t rows1, int K) {
     const int b = (int)blockIdx.x;
@@ -80,20 +82,33 @@ __global__ void __launch_bounds__(256) prep_norms_kernel(
                   ticket, err, rows, nwords, lo, hi);
         return;
     }
-    norms_at((int64_t)(b - prep_blocks) * blockDim.x + threadIdx.x, v0, out0, rows0, v1, out1,
-             rows1, K);
+    if (b < prep_blocks + zero_blocks) {
+        const int64_t stride = (int64_t)zero_blocks * blockDim.x;
+        const int64_t idx = (int64_t)(b - prep_blocks) * blockDim.x + threadIdx.x;
+        for (int64_t k = idx; k < n0; k += stride) z0[k] = 0u;
+        for (int64_t k = idx; k < n1; k += stride) z1[k] = 0u;
+        return;
+    }
+    norms_at((int64_t)(b - prep_blocks - zero_blocks) * blockDim.x + threadIdx.x, v0, out0, rows0,
+             v1, out1, rows1, K);
 }
 
 hipError_t launch_prep_norms(int* ticket, int* err, unsigned long long* rows, int64_t nwords,
                              unsigned long long lo, unsigned long long hi, const float* x,
                              float* x2, int64_t rows_x, const float* y, float* y2,
-                             int64_t rows_y, int K, hipStream_t st) {
+                             int64_t rows_y, int K, unsigned* z0, int64_t n0, unsigned* z1,
+                             int64_t n1, hipStream_t st) {
     int64_t prep = (nwords + 255) / 256;
     prep = prep < 1 ? 1 : (prep > 1024 ? 1024 : prep);
+    if (!z0) n0 = 0;
+    if (!z1) n1 = 0;
+    const int64_t nz = n0 > n1 ? n0 : n1;
+    int64_t zero = (nz + 255) / 256;
+    zero = zero > 1024 ? 1024 : zero;
     const int64_t norm_blocks = ((rows_x + rows_y) * 8 + 255) / 256;
-    hipLaunchKernelGGL(prep_norms_kernel, dim3((unsigned)(prep + norm_blocks)), dim3(256), 0, st,
-                       ticket, err, rows, nwords, lo, hi, (int)prep, x, x2, rows_x, y, y2, rows_y,
-                       K);
+    hipLaunchKernelGGL(prep_norms_kernel, dim3((unsigned)(prep + zero + norm_blocks)), dim3(256), 0,
+                       st, ticket, err, rows, nwords, lo, hi, (int)prep, (int)zero, z0, n0, z1, n1,
+                       x, x2, rows_x, y, y2, rows_y, K);
     return hipGetLastError();
 }
 

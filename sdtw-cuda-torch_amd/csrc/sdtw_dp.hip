@@ -17,10 +17,13 @@ hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st) {
     const int64_t nwords = bwd ? 2 * entries : entries;
     const unsigned long long lo = bwd ? (unsigned long long)kEmpty32 : kEmpty64;
     const unsigned long long hi = bwd ? 0ull : kEmpty64;
-    if (P.x2_fill)  // with the fused recursions' row norms
+    if (P.x2_fill) {  // with the fused recursions' row norms (and the gradient mode's zeroing)
+        const int64_t ngy = bwd && P.gy_out ? (int64_t)P.B * P.M * P.K : 0;
         return launch_prep_norms(P.ticket, P.err, reinterpret_cast<unsigned long long*>(P.gring),
                                  nwords, lo, hi, P.x, P.x2_fill, (int64_t)P.B * P.N, P.y,
-                                 P.y2_fill, (int64_t)P.B * P.M, P.K, st);
+                                 P.y2_fill, (int64_t)P.B * P.M, P.K,
+                                 reinterpret_cast<unsigned*>(P.gy_out), ngy, nullptr, 0, st);
+    }
     int64_t blocks = (nwords + 255) / 256;
     blocks = blocks < 1 ? 1 : (blocks > 2048 ? 2048 : blocks);
     hipLaunchKernelGGL(prep_kernel, dim3((unsigned)blocks), dim3(256), 0, st, P.ticket, P.err,

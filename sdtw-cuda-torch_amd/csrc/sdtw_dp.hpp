@@ -153,9 +153,24 @@ SDTW_DEV void give_up_bwd(const DPParams& P, int p, int b) {
     const int r0 = b * 64;
     const int nrows = min(P.N - r0, 64);
     if (nrows <= 0) return;
-    float* base = P.G_out + ((int64_t)p * P.N + r0) * P.M;
-    const int64_t cells = (int64_t)nrows * P.M;
-    for (int64_t e = threadIdx.x & 63; e < cells; e += 64) base[e] = __builtin_nanf("");
+    const float qnan = __builtin_nanf("");
+    if (P.G_out) {
+        float* base = P.G_out + ((int64_t)p * P.N + r0) * P.M;
+        const int64_t cells = (int64_t)nrows * P.M;
+        for (int64_t e = threadIdx.x & 63; e < cells; e += 64) base[e] = qnan;
+    }
+    // gradient mode: the band's rows of dL/dx, and all of the pair's dL/dy (added, since the
+    // other bands add their tiles to it: NaN + v stays NaN whatever the order)
+    if (P.gx_out) {
+        float* base = P.gx_out + ((int64_t)p * P.N + r0) * P.K;
+        const int64_t n = (int64_t)nrows * P.K;
+        for (int64_t e = threadIdx.x & 63; e < n; e += 64) base[e] = qnan;
+    }
+    if (P.gy_out) {
+        float* base = P.gy_out + (int64_t)p * P.M * P.K;
+        const int64_t n = (int64_t)P.M * P.K;
+        for (int64_t e = threadIdx.x & 63; e < n; e += 64) unsafeAtomicAdd(base + e, qnan);
+    }
 }
 template <bool BWD>
 SDTW_DEV void give_up(const DPParams& P, int p, int b) {
@@ -594,6 +609,9 @@ struct Smem {
     // column of a produced cost tile holding a non-finite cost, per band (ints 40 .. 43)
     SDTW_DEV int* poison_in() const { return reinterpret_cast<int*>(base) + 32; }
     SDTW_DEV int* bad_col() const { return reinterpret_cast<int*>(base) + 40; }
+    // backward, gradient mode: G tiles copied out of the band's cost ring by its gradient
+    // waves, for dL/dx (ints 48 .. 51) and for dL/dy (ints 52 .. 55)
+    SDTW_DEV int* gdone() const { return reinterpret_cast<int*>(base) + 48; }
     SDTW_DEV double* tables() const { return reinterpret_cast<double*>(base + 256); }
     SDTW_DEV unsigned char* ring() const { return base + 256 + tab_bytes; }
     SDTW_DEV float* cost_ring(int w) const {
@@ -664,13 +682,20 @@ struct GTile {
 // (its B operand, or its D values) right after the store.  In the backward the G tile of
 // group t - 4 is read from the slots before they are reused and stored after those loads;
 // the last groups' tiles are stored after the loop.
-template <class Src, bool BWD>
+//
+// Gradient mode (GRAD, backward only): the band's gradient waves copy each G tile out of the
+// slots instead, counting the tiles in gdone (one count per gradient part); the producer
+// then waits for both counts >= t - 3 (which implies done >= t - 3) and stores no G tile.
+template <class Src, bool BWD, bool GRAD = false>
 SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int w) {
     constexpr bool MMA = !std::is_same<Src, CostD>::value;
+    static_assert(!GRAD || (BWD && MMA), "gradient mode: fused backward only");
     Src c;
     c.init(P, p, b);
     float* ring = sm.cost_ring(w);
-    const int* done = sm.done() + w;
+    const int* done = GRAD ? sm.gdone() + w : sm.done() + w;
+    const int* done_y = sm.gdone() + 4 + w;  // gradient mode: the second part's count
+    int known_y = 0;
     int* ready = sm.ready() + w;
     int known = 0;
     bool marked = false;  // the band's first non-finite cost tile has been published
@@ -685,12 +710,13 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
             for (int kk = 0; kk < Src::NKK; ++kk) c.mma(kk);
         }
         const int need = BWD ? t - 3 : t - 4;
-        if (need > 0 && !wait_at_least(done, need, known, P.err, P.spin_limit)) {
+        if (need > 0 && (!wait_at_least(done, need, known, P.err, P.spin_limit) ||
+                         (GRAD && !wait_at_least(done_y, need, known_y, P.err, P.spin_limit)))) {
             give_up<BWD>(P, p, b);
             return;
         }
         GTile gt;
-        const bool flush = BWD && t >= 4;
+        const bool flush = BWD && !GRAD && t >= 4;
         if (flush) gt.read(P, ring, (t - 4) * U);
         if constexpr (MMA) c.finish(ring, col(t));
         else c.store(ring, col(t));
@@ -710,7 +736,7 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
         }
         if (flush) gt.write(P, p, b);
     }
-    if (BWD) {
+    if (BWD && !GRAD) {
         for (int g = max(T - 4, 0); g < groups; ++g) {
             if (!wait_at_least(done, g + 1, known, P.err, P.spin_limit)) {
                 give_up<BWD>(P, p, b);
@@ -719,6 +745,216 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
             GTile gt;
             gt.read(P, ring, g * U);
             gt.write(P, p, b);
+        }
+    }
+}
+
+// Gradient waves of band b (fused backward, gradient mode).  The gradients of the
+// squared-Euclidean cost follow from E (here g*E, the upstream gradient applied) as in the
+// reference's autograd (autograd_xy.py:41-49):
+//   dL/dx_i = 2 (x_i sum_j E_ij - sum_j E_ij y_j),   dL/dy_j = 2 (y_j sum_i E_ij - sum_i E_ij x_i),
+// formed here from the G tiles without materialising E.  The G tile of group g (the band's
+// 64 rows, columns c0 = M + 47 - 16 g .. c0 + 15) is copied out of the band's cost ring as
+// soon as the compute wave has finished the group, and counted (gdone), after which the
+// producer may reuse the slots.  On the matrix cores,
+//   * part X accumulates E Y for the band's rows over all tiles (A = E[16 rb + (l & 15)]
+//     [c0 + 4 kk + (l >> 4)], B = y[c0 + 4 kk + (l >> 4)][16 fb + (l & 15)]) with the row
+//     sums, and writes dL/dx once at the end;
+//   * part Y forms the tile's E^T X (A = E[4 kk + (l >> 4)][c0 + (l & 15)], the G tile's own
+//     layout; B = x[row0 + 4 kk + (l >> 4)][16 fb + (l & 15)], kept in registers) and column
+//     sums, and adds the band's share 2 (y cs - E^T X) to dL/dy (zeroed by the prep launch)
+//     with fire-and-forget atomics.  The bands' shares of an entry therefore meet in the
+//     order they arrive: dL/dy can differ in the last bits between runs (dL/dx cannot).
+//     Ordering the bands (each waiting for the band below to flag a tile once its additions
+//     have returned) costs more than the whole recursion at wide features: the returns and
+//     the flag polls sit in every tile of the chain.  Callers that need run-to-run identical
+//     bits take the E path (sdtw_set_deterministic).
+// One wave does both parts (PART 3), or two waves one each (PART 1, 2), each with its own
+// count (gdone x / y).  The next tile's y operands are loaded before the wait for the
+// compute wave, so no memory latency sits between two tiles.  Entries of a tile outside
+// the table (rows >= N, columns outside [0, M)) are zeroed.  Waits are bounded; a wave that
+// gives up marks the pair's results NaN.
+constexpr int kGradPartX = 1, kGradPartY = 2;
+constexpr int kGdoneIdle = 1 << 30;  // count of a part with nothing to do
+
+template <int KX, int PART>
+SDTW_DEV void grad_wave(const DPParams& P, const Smem& sm, int p, int b, int w) {
+    constexpr int FB = KX >= 16 ? KX / 16 : 1;  // 16-feature blocks of the outputs
+    constexpr bool HAS_X = (PART & kGradPartX) != 0, HAS_Y = (PART & kGradPartY) != 0;
+    const int l = threadIdx.x & (WAVE - 1);
+    const int li = l & 15, lq = l >> 4;
+    int* gdx = sm.gdone() + w;
+    int* gdy = sm.gdone() + 4 + w;
+    const bool want_gx = HAS_X && P.gx_out != nullptr;
+    const bool want_gy = HAS_Y && P.gy_out != nullptr;
+    if (!want_gx && !want_gy) {  // nothing to form: the producer need not wait for this wave
+        if (l == 0) {
+            if (HAS_X) lds_publish(gdx, kGdoneIdle);
+            if (HAS_Y) lds_publish(gdy, kGdoneIdle);
+        }
+        return;
+    }
+    if (l == 0) {  // a part this wave owns but does not form
+        if (HAS_X && !want_gx) lds_publish(gdx, kGdoneIdle);
+        if (HAS_Y && !want_gy) lds_publish(gdy, kGdoneIdle);
+    }
+    const int N = P.N, M = P.M, K = P.K;
+    const int row0 = b * WAVE;
+    const int groups = P.S / U;
+    const float* x = P.x + (int64_t)p * N * K;
+    const float* y = P.y + (int64_t)p * M * K;
+    const float* cring = sm.cost_ring(w);
+    const int* done = sm.done() + w;
+    float* gy = want_gy ? P.gy_out + (int64_t)p * M * K : nullptr;
+
+    float xB[HAS_Y ? 16 : 1][FB];
+    if constexpr (HAS_Y) {
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+            for (int fb = 0; fb < FB; ++fb) {
+                const int row = row0 + 4 * kk + lq, f = 16 * fb + li;
+                xB[kk][fb] = (want_gy && row < N && f < K) ? x[(int64_t)row * K + f] : 0.0f;
+            }
+    }
+    floatx4 gacc[HAS_X ? 4 : 1][FB];
+    float rsp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (HAS_X) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int fb = 0; fb < FB; ++fb) gacc[rb][fb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    // the y operands of tile g: B of E Y (yb) and the y of 2 (y cs - E^T X) (yc)
+    auto live_tile = [&](int g) { const int c0 = M + 47 - g * U; return c0 < M && c0 + 15 >= 0; };
+    auto load_y = [&](int g, float (&yb)[4][FB], float (&yc)[4][FB]) {
+        const int c0 = M + 47 - g * U;
+        const bool live = g < groups && live_tile(g);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int fb = 0; fb < FB; ++fb) {
+                const int f = 16 * fb + li;
+                const int cb = c0 + 4 * q + lq, cc = c0 + 4 * lq + q;
+                const bool okb = HAS_X && live && want_gx && (unsigned)cb < (unsigned)M && f < K;
+                const bool okc = HAS_Y && live && want_gy && (unsigned)cc < (unsigned)M && f < K;
+                yb[q][fb] = okb ? y[(int64_t)cb * K + f] : 0.0f;
+                yc[q][fb] = okc ? y[(int64_t)cc * K + f] : 0.0f;
+            }
+    };
+    float yBn[4][FB], yCn[4][FB];
+    load_y(0, yBn, yCn);
+    int known = 0;
+    for (int g = 0; g < groups; ++g) {
+        const int c0 = M + 47 - g * U;
+        const bool live = live_tile(g);
+        float yB[4][FB], yC[4][FB];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int fb = 0; fb < FB; ++fb) {
+                yB[q][fb] = yBn[q][fb];
+                yC[q][fb] = yCn[q][fb];
+            }
+        load_y(g + 1, yBn, yCn);
+        if (!wait_at_least(done, g + 1, known, P.err, P.spin_limit)) {
+            give_up_bwd(P, p, b);
+            return;
+        }
+        float eT[HAS_Y ? 16 : 1], eA[HAS_X ? 4 : 1][4];
+        if constexpr (HAS_Y) {
+            const int ct = c0 + li;
+            const bool ct_ok = live && (unsigned)ct < (unsigned)M;
+            const float* src = cring + lq * CS + (ct & (CR - 1));
+#pragma unroll
+            for (int k = 0; k < 16; ++k) eT[k] = (ct_ok && row0 + 4 * k + lq < N) ? src[4 * k * CS] : 0.0f;
+        }
+        if constexpr (HAS_X) {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int ca = c0 + 4 * kk + lq;
+                const bool ca_ok = live && (unsigned)ca < (unsigned)M;
+                const float* srcA = cring + li * CS + (ca & (CR - 1));
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+                    eA[rb][kk] = (ca_ok && row0 + 16 * rb + li < N) ? srcA[16 * rb * CS] : 0.0f;
+            }
+        }
+        // the slots may be reused once these reads are performed (LDS operations of a wave
+        // are performed in order, the count after them)
+        if (l == 0) {
+            if (want_gx) lds_publish(gdx, g + 1);
+            if (want_gy) lds_publish(gdy, g + 1);
+        }
+        if (!live) continue;
+        if constexpr (HAS_X) {
+            if (want_gx) {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                        for (int fb = 0; fb < FB; ++fb)
+                            gacc[rb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(eA[rb][kk], yB[kk][fb], gacc[rb][fb], 0, 0, 0);
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) rsp[rb] += (eA[rb][0] + eA[rb][1]) + (eA[rb][2] + eA[rb][3]);
+            }
+        }
+        if constexpr (HAS_Y) {
+            if (want_gy) {
+                floatx4 pg[FB];
+#pragma unroll
+                for (int fb = 0; fb < FB; ++fb) pg[fb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+                    for (int fb = 0; fb < FB; ++fb)
+                        pg[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(eT[kk], xB[kk][fb], pg[fb], 0, 0, 0);
+                // column sums: lane l holds rows 4 k + (l >> 4) of column c0 + (l & 15)
+                float cs = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) cs += eT[k];
+                cs += __shfl_xor(cs, 16);
+                cs += __shfl_xor(cs, 32);
+                float csr[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) csr[r] = __shfl(cs, 4 * lq + r);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int fb = 0; fb < FB; ++fb) {
+                        const int col = c0 + 4 * lq + r, f = 16 * fb + li;
+                        if ((unsigned)col < (unsigned)M && f < K)
+                            (void)unsafeAtomicAdd(gy + (int64_t)col * K + f,
+                                                  2.0f * (yC[r][fb] * csr[r] - pg[fb][r]));
+                    }
+            }
+        }
+    }
+    if constexpr (HAS_X) {
+        if (want_gx) {
+            float* gx = P.gx_out + (int64_t)p * N * K;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                // lanes l, l ^ 16, l ^ 32, l ^ 48 hold the four column quarters of row
+                // 16 rb + (l & 15)
+                float rs = rsp[rb];
+                rs += __shfl_xor(rs, 16);
+                rs += __shfl_xor(rs, 32);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float rsr = __shfl(rs, 4 * lq + r);
+                    const int row = row0 + 16 * rb + 4 * lq + r;
+#pragma unroll
+                    for (int fb = 0; fb < FB; ++fb) {
+                        const int f = 16 * fb + li;
+                        if (row < N && f < K) {
+                            const int64_t e = (int64_t)row * K + f;
+                            gx[e] = 2.0f * (x[e] * rsr - gacc[rb][fb][r]);
+                        }
+                    }
+                }
+            }
         }
     }
 }
@@ -1250,8 +1486,23 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         if (!group(q0, std::false_type{})) return give_up_bwd(P, p, b);
 }
 
-template <class Cost, bool BAND, bool EXACT>
-__global__ void __launch_bounds__((dp_threads<Cost, true>())) bwd_kernel(DPParams P) {
+template <class C>
+struct KXOf : std::integral_constant<int, 0> {};
+template <int KX>
+struct KXOf<CostMfma<KX>> : std::integral_constant<int, KX> {};
+
+// GW > 0: gradient mode for workgroups of up to GW bands.  GW = 2: waves compute 0 .. W-1,
+// producers W .. 2W-1, dL/dy waves 2W .. 3W-1, dL/dx waves 3W .. 4W-1, helper 4W (under
+// round-robin placement with W = 2 the dL/dy waves share the compute waves' SIMDs and the
+// dL/dx waves the producers'; measured faster than the other way round, whose dL/dx
+// products then sit beside the recursion).  GW = 4 (widths <= 16, whose gradient work is
+// light): one gradient wave per band, 2W .. 3W-1, helper 3W.
+template <int GW>
+constexpr int grad_waves_per_band() { return GW == 2 ? 4 : 3; }
+template <class Cost, bool BAND, bool EXACT, int GW = 0>
+__global__ void __launch_bounds__((GW ? (grad_waves_per_band<GW>() * GW + 1) * WAVE : dp_threads<Cost, true>()))
+bwd_kernel(DPParams P) {
+    static_assert(GW == 0 || KXOf<Cost>::value > 0, "gradient mode needs matrix-core cost tiles");
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W), kTabBytesBwd};
     // wave-uniform values are moved to scalar registers so that the branches on band,
@@ -1260,17 +1511,35 @@ __global__ void __launch_bounds__((dp_threads<Cost, true>())) bwd_kernel(DPParam
     if (threadIdx.x == 0) *sm.ticket() = atomicAdd(P.ticket, 1);
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;
     if (threadIdx.x < 16) sm.ready()[threadIdx.x] = 0;
+    if (threadIdx.x < 8) sm.gdone()[threadIdx.x] = 0;
     sm.load_tables();
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G;
     const int g = (P.G - 1) - (t - p * P.G);  // lowest ticket of a pair takes the bottom group
-    if (w == (Produced<Cost, true>::value ? 2 * P.W : P.W)) {
+    const int helper = GW ? grad_waves_per_band<GW>() * P.W : (Produced<Cost, true>::value ? 2 * P.W : P.W);
+    if (w == helper) {
         // helper wave: the next workgroup's first row into ring W
         if (g + 1 < P.G) helper_wave(P, sm, P.gring4 + ((int64_t)p * P.G + (g + 1)) * P.RW + RPAD, P.W);
         return;
     }
-    if constexpr (Produced<Cost, true>::value) {
+    if constexpr (GW > 0) {
+        const int role = w >= 3 * P.W ? 3 : (w >= 2 * P.W ? 2 : (w >= P.W ? 1 : 0));
+        const int wb = w - role * P.W;
+        if (g * P.W + wb >= P.nb) return;
+        if (role == 3) {
+            grad_wave<KXOf<Cost>::value, kGradPartX>(P, sm, p, g * P.W + wb, wb);
+        } else if (role == 2) {
+            if constexpr (GW == 2) grad_wave<KXOf<Cost>::value, kGradPartY>(P, sm, p, g * P.W + wb, wb);
+            else grad_wave<KXOf<Cost>::value, kGradPartX | kGradPartY>(P, sm, p, g * P.W + wb, wb);
+        } else if (role == 1) {
+            producer_wave<Cost, true, true>(P, sm, p, g * P.W + wb, wb);
+        } else {
+            CostRing cost;
+            cost.bind(sm, w, P);
+            bwd_band<CostRing, BAND, EXACT>(P, cost, sm, p, g, w);
+        }
+    } else if constexpr (Produced<Cost, true>::value) {
         const int wb = w >= P.W ? w - P.W : w;
         if (g * P.W + wb >= P.nb) return;
         if (w >= P.W) {
@@ -1300,7 +1569,8 @@ inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
 }
 
 template <class K>
-hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipStream_t st) {
+hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipStream_t st,
+                     bool grad = false) {
     const size_t lds = dp_smem_bytes(P, bwd);
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -1311,7 +1581,7 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipSt
     if (e != hipSuccess) return e;
     // one wave per band, plus a helper wave when a pair spans several workgroups; with
     // matrix-core costs, the helper slot and one producer wave per band
-    const int waves = produced ? 2 * P.W + 1 : P.W + (P.G > 1 ? 1 : 0);
+    const int waves = grad ? (P.W <= 2 ? 4 : 3) * P.W + 1 : (produced ? 2 * P.W + 1 : P.W + (P.G > 1 ? 1 : 0));
     hipLaunchKernelGGL(kernel, dim3(P.B * P.G), dim3(waves * WAVE), lds, st, P);
     return hipGetLastError();
 }
@@ -1327,6 +1597,27 @@ hipError_t launch_cost(const DPParams& P, hipStream_t st) {
     }
 }
 
+// Fused backward in gradient mode (P.gx_out or P.gy_out set, P.G_out null): workgroups of up
+// to 2 bands for any matrix-core width, up to 4 for widths <= 16 (their waves fit 128
+// registers).  Instantiated in sdtw_dp_bwd_grad_*.hip.
+template <bool EXACT>
+hipError_t launch_dp_grad(const DPParams& P, hipStream_t st);
+
+template <class Cost, bool EXACT>
+hipError_t launch_grad_cost(const DPParams& P, hipStream_t st) {
+    if (P.W <= 2) {
+        if (P.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT, 2>, P, true, true, st, true);
+        return launch_dp(bwd_kernel<Cost, false, EXACT, 2>, P, true, true, st, true);
+    }
+    if constexpr (KXOf<Cost>::value <= 16) {
+        if (P.W <= 4) {
+            if (P.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT, 4>, P, true, true, st, true);
+            return launch_dp(bwd_kernel<Cost, false, EXACT, 4>, P, true, true, st, true);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
 // One (direction, arithmetic, cost source) family of kernels.  Fused kernels take the
 // matrix-core cost tiles, with x rows in registers padded to the smallest of 4, 8, 16, 32,
 // 64 >= K; wider features, and the tiny problems whose reference dot is a multiply-then-add,
@@ -1337,6 +1628,10 @@ hipError_t launch_dp_variant(const DPParams& P, bool muladd, hipStream_t st) {
         (void)muladd;
         return launch_cost<CostD, BWD, EXACT>(P, st);
     } else {
+        if (BWD && (P.gx_out || P.gy_out)) {
+            if (muladd || P.K > 64) return hipErrorInvalidValue;
+            return launch_dp_grad<EXACT>(P, st);
+        }
         if (muladd) return launch_cost<CostScalar<true>, BWD, EXACT>(P, st);
         if (P.K <= 4) return launch_cost<CostMfma<4>, BWD, EXACT>(P, st);
         if (P.K <= 8) return launch_cost<CostMfma<8>, BWD, EXACT>(P, st);
@@ -1361,5 +1656,17 @@ hipError_t launch_dp_variant(const DPParams& P, bool muladd, hipStream_t st) {
     extern template hipError_t launch_dp_variant<B, E, F>(const DPParams&, bool, hipStream_t);
 SDTW_DP_VARIANTS(SDTW_DP_EXTERN)
 #undef SDTW_DP_EXTERN
+extern template hipError_t launch_dp_grad<false>(const DPParams&, hipStream_t);
+extern template hipError_t launch_dp_grad<true>(const DPParams&, hipStream_t);
+
+// the gradient-mode dispatch over the matrix-core widths (defined where instantiated)
+template <bool EXACT>
+hipError_t launch_dp_grad(const DPParams& P, hipStream_t st) {
+    if (P.K <= 4) return launch_grad_cost<CostMfma<4>, EXACT>(P, st);
+    if (P.K <= 8) return launch_grad_cost<CostMfma<8>, EXACT>(P, st);
+    if (P.K <= 16) return launch_grad_cost<CostMfma<16>, EXACT>(P, st);
+    if (P.K <= 32) return launch_grad_cost<CostMfma<32>, EXACT>(P, st);
+    return launch_grad_cost<CostMfma<64>, EXACT>(P, st);
+}
 
 }  // namespace sdtw

@@ -1,0 +1,6 @@
+// Instantiates the fused backward's gradient-mode kernels, exact arithmetic (sdtw_dp.hpp).
+#include "sdtw_dp.hpp"
+
+namespace sdtw {
+template hipError_t launch_dp_grad<true>(const DPParams&, hipStream_t);
+}  // namespace sdtw

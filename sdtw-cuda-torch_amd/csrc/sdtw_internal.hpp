@@ -18,7 +18,12 @@ struct DPParams {
     const float* y2;    // fused: row norms (B,M)
     float* R;           // band-skewed table: forward writes, backward reads
     float* out;         // (B) forward result
-    float* G_out;       // backward: (B,N,M) = gout * E
+    float* G_out;       // backward: (B,N,M) = gout * E, or nullptr (gradient mode)
+    // Fused backward, gradient mode (G_out null): the gradients formed in the kernel from the
+    // E tiles, never materialising (B,N,M).  gx_out: dL/dx (B,N,K); gy_out: dL/dy (B,M,K),
+    // zeroed by the prep launch and accumulated band by band.  Null = not wanted.
+    float* gx_out;
+    float* gy_out;
     const float* gout;  // backward: (B) upstream gradient or nullptr (= 1)
     float* D_out;       // fused forward: the cost tiles also stored here (B,N,M), or nullptr
     float* x2_fill;     // fused: x2 / y2 (writable) for the prep launch to form, or nullptr
@@ -105,12 +110,14 @@ __device__ inline void prep_rows(int64_t idx, int64_t stride, int* ticket, int* 
     }
     for (int64_t k = idx; k < nwords; k += stride) rows[k] = (k & 1) ? hi : lo;
 }
-// The prep work and the row norms of x and y in one launch (the fused recursions need both
-// before they start).
+// The prep work, the row norms of x and y, and the zeroing of up to two ranges of 32-bit
+// words (z0: n0 words, z1: n1 words; null or 0 = none) in one launch (the fused recursions
+// need all of it before they start).
 hipError_t launch_prep_norms(int* ticket, int* err, unsigned long long* rows, int64_t nwords,
                              unsigned long long lo, unsigned long long hi, const float* x,
                              float* x2, int64_t rows_x, const float* y, float* y2,
-                             int64_t rows_y, int K, hipStream_t st);
+                             int64_t rows_y, int K, unsigned* z0, int64_t n0, unsigned* z1,
+                             int64_t n1, hipStream_t st);
 hipError_t launch_norms(const float* x, float* x2, int64_t rows_x, const float* y, float* y2,
                         int64_t rows_y, int K, hipStream_t st);
 hipError_t launch_dist(const DistParams& p, bool muladd, bool mfma, hipStream_t st);

@@ -31,6 +31,7 @@ _SIGS = {
     "sdtw_set_numerics": ([ctypes.c_int], ctypes.c_int),
     "sdtw_get_numerics": ([], ctypes.c_int),
     "sdtw_set_wait_limit": ([ctypes.c_uint], ctypes.c_uint),
+    "sdtw_set_deterministic": ([ctypes.c_int], ctypes.c_int),
     "sdtw_fused_bands_per_workgroup": ([ctypes.c_int64] * 4, ctypes.c_int),
     "sdtw_workspace_bytes": ([ctypes.c_int] + [ctypes.c_int64] * 4, ctypes.c_size_t),
     "sdtw_table_elems": ([ctypes.c_int64] * 3, ctypes.c_int64),
@@ -135,6 +136,21 @@ def set_wait_limit(polls: int) -> int:
     """Polls a wavefront kernel's bounded wait makes before giving up (process-wide); returns
     the previous limit.  A test hook: a wave that gives up marks its pair's results NaN."""
     return int(load().sdtw_set_wait_limit(int(polls)))
+
+
+_deterministic = None  # the library's setting as last set from here
+
+
+def sync_deterministic() -> bool:
+    """Make the library's fused-backward choice follow torch.use_deterministic_algorithms():
+    under it, sdtw_fused_bwd_f32 takes its E path (run-to-run identical bits) instead of
+    forming dL/dy with atomics in the recursion kernel.  Returns the setting."""
+    global _deterministic
+    want = bool(torch.are_deterministic_algorithms_enabled())
+    if want != _deterministic:
+        load().sdtw_set_deterministic(int(want))
+        _deterministic = want
+    return want
 
 
 def strerror(rc: int) -> str:
@@ -404,6 +420,7 @@ def fused_bwd(x, y, R, gamma: float, bandwidth: float, gout=None, need=(True, Tr
     M = y.shape[1]
     gx = torch.empty_like(x) if need[0] else None
     gy = torch.empty_like(y) if need[1] else None
+    sync_deterministic()
     ws, nws = _workspace(OP_FUSED_BWD, B, N, M, K, x.device)
     with torch.cuda.device(x.device):
         rc = load().sdtw_fused_bwd_f32(_ptr(x), _ptr(y), _ptr(R), _ptr(gout), _ptr(gx), _ptr(gy),

@@ -56,7 +56,17 @@ def test_workspace_sizes():
     lib = _engine.load()
     B, N, M, K = 32, 512, 512, 64
     assert lib.sdtw_workspace_bytes(_engine.OP_FWD, B, N, M, K) >= 8 * B * M
-    assert lib.sdtw_workspace_bytes(_engine.OP_FUSED_BWD, B, N, M, K) >= 4 * B * N * M
+    # the fused backward forms the gradients in the recursion kernel with matrix-core costs:
+    # its workspace holds nothing of (B, N, M) size (norms, row scratch, one flag per tile)
+    assert lib.sdtw_workspace_bytes(_engine.OP_FUSED_BWD, B, N, M, K) < B * N * M * 4 // 8
+    # wider features take the scalar cost tiles, whose backward reduces g*E from the workspace
+    assert lib.sdtw_workspace_bytes(_engine.OP_FUSED_BWD, B, N, M, 96) >= 4 * B * N * M
+    # so does every fused backward forming dL/dy under the deterministic setting
+    prev = lib.sdtw_set_deterministic(1)
+    try:
+        assert lib.sdtw_workspace_bytes(_engine.OP_FUSED_BWD, B, N, M, K) >= 4 * B * N * M
+    finally:
+        lib.sdtw_set_deterministic(prev)
     assert lib.sdtw_workspace_bytes(99, B, N, M, K) == 0
 
 
