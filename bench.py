@@ -97,11 +97,17 @@ def kernel_launcher(name, xg, yg, gamma):
     D = _engine.sqeuclid_fwd(xg, yg)
     out, R = _engine.dtw_fwd(D, gamma, -1.0)
     G = _engine.dtw_bwd(D, R, gamma, -1.0)
+    # the distance backward as the unfused module runs it: with the one-launch forward's
+    # distance record where that forward is taken
+    B_, N_, K_ = xg.shape
+    M_ = yg.shape[1]
+    record = (_engine.fused_fwd_d(xg, yg, gamma, -1.0)[3]
+               if _engine.one_launch_unfused_forward(B_, N_, M_, K_, xg.device) else None)
     fn = {
         "dist_fwd": lambda: _engine.sqeuclid_fwd(xg, yg),
         "dp_fwd": lambda: _engine.dtw_fwd(D, gamma, -1.0),
         "dp_bwd": lambda: _engine.dtw_bwd(D, R, gamma, -1.0),
-        "dist_bwd": lambda: _engine.sqeuclid_bwd(xg, yg, D, G, mask=True),
+        "dist_bwd": lambda: _engine.sqeuclid_bwd(xg, yg, D, G, mask=True, record=record),
         "fused_fwd": lambda: _engine.fused_fwd(xg, yg, gamma, -1.0),
         "fused_fwd_d": lambda: _engine.fused_fwd_d(xg, yg, gamma, -1.0),
         "fused_bwd_e": lambda: _engine.fused_bwd_e(xg, yg, R, gamma, -1.0),

@@ -114,6 +114,10 @@ int sdtw_debug_status(int op, const void *ws, size_t ws_bytes, int64_t B, int64_
  * counterpart in the reference. */
 unsigned sdtw_set_wait_limit(unsigned polls);
 
+/* Bytes of the distance record sdtw_fused_fwd_d_f32 can write for sdtw_sqeuclid_bwd_f32
+ * (per-pair clamp flags and row norms; device memory the caller owns). */
+size_t sdtw_dist_record_bytes(int64_t B, int64_t N, int64_t M);
+
 /* Process-wide: 1 makes sdtw_fused_bwd_f32 give run-to-run identical bits by taking its
  * E path (g*E in the workspace, reduced by the distance backward); 0 (the default) lets it
  * form the gradients inside the recursion kernel, whose dL/dy adds the bands' shares with
@@ -154,13 +158,17 @@ int sdtw_sqeuclid_fwd_f32(const float *x, const float *y, float *D, int64_t B, i
  *   G' = G where (x2 + y2 - 2xy) >= 0 else 0            (clamp_min backward)
  *   gx = 2 (x * rowsum(G') - G' y),  gy = 2 (y * colsum(G') - G'^T x)
  * D is the clamped forward output (used to find clamped cells).  mask = 0 skips the clamp
- * mask (the fused-mode chain rule of autograd_xy.py:45-49 has none).  gx or gy may be NULL:
- * that gradient is not formed (autograd's needs_input_grad); both NULL is a no-op.
+ * mask (the fused-mode chain rule of autograd_xy.py:45-49 has none).  record: NULL, or the
+ * distance record sdtw_fused_fwd_d_f32 wrote with this D: the pairs it records as free of
+ * clamped cells have the identity mask and their D is not read, and its row norms serve the
+ * exact check of the others (no norms launch here).  gx or gy may be NULL: that gradient is
+ * not formed (autograd's needs_input_grad); both NULL is a no-op.  Both gradients with no
+ * mask, or with a record, take one launch for the two reductions.
  * Replaces the torch autograd backward of distances.py:20-28 (bmm/sum/clamp_min
  * backward) and, with mask = 0, autograd_xy.py:41-49. */
-int sdtw_sqeuclid_bwd_f32(const float *x, const float *y, const float *D, const float *G,
-                          float *gx, float *gy, int64_t B, int64_t N, int64_t M, int64_t K,
-                          int mask, void *ws, size_t ws_bytes, void *stream);
+int sdtw_sqeuclid_bwd_f32(const float *x, const float *y, const float *D, const void *record,
+                          const float *G, float *gx, float *gy, int64_t B, int64_t N, int64_t M,
+                          int64_t K, int mask, void *ws, size_t ws_bytes, void *stream);
 
 /* Soft-DTW forward over a materialised cost D (B,N,M): R table and out[b] = R[b,N-1,M-1].
  * Replaces softdtw_cuda/cuda/launcher.py:167-223 (softdtw_forward_cuda) with the
@@ -203,9 +211,13 @@ int sdtw_fused_fwd_f32(const float *x, const float *y, float *R, float *out, int
  * also store every cost tile into D (B,N,M), with the bits sdtw_sqeuclid_fwd_f32(EXACT)
  * writes.  Replaces distances.py:6-28 followed by launcher.py:167-223 (the cost tensor,
  * then the recursion over it).  Workspace as SDTW_OP_FUSED_FWD.  SDTW_ERR_UNSUPPORTED
- * where the costs take scalar tiles (K > 64, or K*N*M < 400): use the two calls there. */
-int sdtw_fused_fwd_d_f32(const float *x, const float *y, float *D, float *R, float *out,
-                         int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
+ * where the costs take scalar tiles (K > 64, or K*N*M < 400): use the two calls there.
+ * record: NULL, or a distance record of sdtw_dist_record_bytes(B, N, M) bytes for
+ * sdtw_sqeuclid_bwd_f32: per pair, whether a cost is not positive (0 or NaN), and the row
+ * norms of x and y (no counterpart in the reference: it lets the distance backward skip
+ * reading D and its norms launch). */
+int sdtw_fused_fwd_d_f32(const float *x, const float *y, float *D, void *record, float *R,
+                         float *out, int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
                          double bandwidth, void *ws, size_t ws_bytes, void *stream);
 
 /* Fused backward: E recomputed with per-cell costs from x, y, then

@@ -114,6 +114,27 @@ size_t ws_dist_bwd(int64_t B, int64_t N, int64_t M, int64_t K) {
            align_up(sizeof(int) * dist_bwd_flags(B, N, M, K));
 }
 
+// Distance record (sdtw_fused_fwd_d_f32 -> sdtw_sqeuclid_bwd_f32): [per-pair clamp flags,
+// B ints][row norms of x, B*N floats][row norms of y, B*M floats], each part 256-byte aligned.
+struct DistRecord {
+    int* clamped;
+    float* x2;
+    float* y2;
+};
+size_t dist_record_bytes(int64_t B, int64_t N, int64_t M) {
+    return align_up(sizeof(int) * B) + align_up(sizeof(float) * B * N) + align_up(sizeof(float) * B * M);
+}
+DistRecord dist_record(void* rec, int64_t B, int64_t N, int64_t M) {
+    (void)M;
+    char* c = static_cast<char*>(rec);
+    DistRecord r{};
+    if (!c) return r;
+    r.clamped = reinterpret_cast<int*>(c);
+    r.x2 = reinterpret_cast<float*>(c + align_up(sizeof(int) * B));
+    r.y2 = reinterpret_cast<float*>(c + align_up(sizeof(int) * B) + align_up(sizeof(float) * B * N));
+    return r;
+}
+
 size_t ws_norms(int64_t B, int64_t N, int64_t M) {
     return align_up(sizeof(float) * B * N) + align_up(sizeof(float) * B * M);
 }
@@ -227,6 +248,11 @@ unsigned sdtw_set_wait_limit(unsigned polls) { return g_spin_limit.exchange(poll
 
 int sdtw_set_deterministic(int on) { return g_deterministic.exchange(on ? 1 : 0); }
 
+size_t sdtw_dist_record_bytes(int64_t B, int64_t N, int64_t M) {
+    if (B < 0 || N < 0 || M < 0) return 0;
+    return dist_record_bytes(B, N, M);
+}
+
 int sdtw_fused_bands_per_workgroup(int64_t B, int64_t N, int64_t M, int64_t K) {
     if (!shape_ok(B, N, M, K, true)) return 0;
     return fused_wmax(B, N, M, K);
@@ -318,9 +344,9 @@ int sdtw_sqeuclid_fwd_f32(const float* x, const float* y, float* D, int64_t B, i
     return status_of(launch_dist(p, small_bmm(N, M, K), false, (hipStream_t)stream));
 }
 
-int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const float* G,
-                          float* gx, float* gy, int64_t B, int64_t N, int64_t M, int64_t K,
-                          int mask, void* ws, size_t ws_bytes, void* stream) {
+int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const void* record,
+                          const float* G, float* gx, float* gy, int64_t B, int64_t N, int64_t M,
+                          int64_t K, int mask, void* ws, size_t ws_bytes, void* stream) {
     if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
     if (B == 0 || (!gx && !gy)) return SDTW_OK;
     if (!x || !y || !G || (mask && !D)) return SDTW_ERR_INVALID_VALUE;
@@ -338,6 +364,8 @@ int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const 
     p.M = (int)M;
     p.K = (int)K;
     p.mask = mask ? 1 : 0;
+    const DistRecord rec = dist_record(const_cast<void*>(record), B, N, M);
+    p.clamped = (mask && record) ? rec.clamped : nullptr;
     p.muladd = small_bmm(N, M, K) ? 1 : 0;
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
@@ -346,7 +374,10 @@ int sdtw_sqeuclid_bwd_f32(const float* x, const float* y, const float* D, const 
     p.cnt = c.take<int>(dist_bwd_counters(B, N, M, K));
     p.flags = c.take<int>(dist_bwd_flags(B, N, M, K));
     if (!c.ok) return SDTW_ERR_WORKSPACE;
-    if (mask) {
+    if (mask && record) {  // the forward formed the norms (the exact clamp check's inputs)
+        p.x2 = rec.x2;
+        p.y2 = rec.y2;
+    } else if (mask) {
         if (launch_norms(x, x2, B * N, y, y2, B * M, (int)K, st) != hipSuccess)
             return SDTW_ERR_LAUNCH;
         p.x2 = x2;
@@ -410,8 +441,8 @@ int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, in
 
 // Fused forward; with D non-null the matrix-core producer waves also store each cost tile
 // into D (B,N,M).
-static int fused_fwd_common(const float* x, const float* y, float* D, float* R, float* out,
-                            int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
+static int fused_fwd_common(const float* x, const float* y, float* D, void* record, float* R,
+                            float* out, int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
                             double bandwidth, void* ws, size_t ws_bytes, void* stream) {
     if (!shape_ok(B, N, M, K, true) || !gamma_ok(gamma)) return SDTW_ERR_INVALID_VALUE;
     if (B == 0) return SDTW_OK;
@@ -434,23 +465,30 @@ static int fused_fwd_common(const float* x, const float* y, float* D, float* R, 
     p.R = R;
     p.out = out;
     p.D_out = D;
+    if (D && record) {  // the distance record: clamp flags, and the norms formed here
+        const DistRecord rec = dist_record(record, B, N, M);
+        p.clamped = rec.clamped;
+        p.x2 = p.x2_fill = rec.x2;
+        p.y2 = p.y2_fill = rec.y2;
+    }
     return status_of(launch_fwd(p, true, small_bmm(N, M, K), exact_forward(), st));
 }
 
 int sdtw_fused_fwd_f32(const float* x, const float* y, float* R, float* out, int64_t B,
                        int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
                        void* ws, size_t ws_bytes, void* stream) {
-    return fused_fwd_common(x, y, nullptr, R, out, B, N, M, K, gamma, bandwidth, ws, ws_bytes,
-                            stream);
+    return fused_fwd_common(x, y, nullptr, nullptr, R, out, B, N, M, K, gamma, bandwidth, ws,
+                            ws_bytes, stream);
 }
 
-int sdtw_fused_fwd_d_f32(const float* x, const float* y, float* D, float* R, float* out,
-                         int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
+int sdtw_fused_fwd_d_f32(const float* x, const float* y, float* D, void* record, float* R,
+                         float* out, int64_t B, int64_t N, int64_t M, int64_t K, double gamma,
                          double bandwidth, void* ws, size_t ws_bytes, void* stream) {
     if (!shape_ok(B, N, M, K, true)) return SDTW_ERR_INVALID_VALUE;
     if (!mfma_costs(N, M, K)) return SDTW_ERR_UNSUPPORTED;  // scalar cost tiles: no producer
     if (B > 0 && !D) return SDTW_ERR_INVALID_VALUE;
-    return fused_fwd_common(x, y, D, R, out, B, N, M, K, gamma, bandwidth, ws, ws_bytes, stream);
+    return fused_fwd_common(x, y, D, record, R, out, B, N, M, K, gamma, bandwidth, ws, ws_bytes,
+                            stream);
 }
 
 // Fused backward core: norms (formed by the prep launch), then the reverse wavefront writing
@@ -592,8 +630,8 @@ int sdtw_barycenter_f32(const float* X, const float* w, float* bary, float* loss
         // losses of the barycenter (xb: its copy per pair) against every sequence, and
         // d loss / d barycenter per pair (the backward's upstream gradient is the weights;
         // dL/dX is not formed)
-        int rc = fused_fwd_common(xb, X, nullptr, R, out, B, N, N, K, gamma, -1.0, rec, rec_bytes,
-                                  stream);
+        int rc = fused_fwd_common(xb, X, nullptr, nullptr, R, out, B, N, N, K, gamma, -1.0, rec,
+                                  rec_bytes, stream);
         if (rc != SDTW_OK) return rc;
         rc = sdtw_fused_bwd_f32(xb, X, R, w, gx, nullptr, B, N, N, K, gamma, -1.0, rec, rec_bytes,
                                 stream);

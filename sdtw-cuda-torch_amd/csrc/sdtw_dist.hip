@@ -432,27 +432,24 @@ constexpr int ZBUF = 64 * ZS;  // floats per Z buffer
 // stores), waits for them to complete and counts itself in the tile's counter; the last
 // piece to arrive adds the ST partials in order 0..ST-1 (deterministic), writes the
 // gradient and resets the counter to zero for the next launch.
+struct DistBwdSmem {
+    float gbuf[2][GBUF];
+    float zbuf[2][ZBUF];
+    int last_piece;
+};
+
+// One output tile: pair b, row strip by (64 rows of gx, or of gy when TRANS), feature tile
+// bx (KT features), reduction piece st of ST.  ntx / nty: feature tiles / row strips of the
+// pass (the tile's index among the pass's tiles).  flag_id: this workgroup's slot in
+// p.flags (the gx pass of a masked two-launch call), or -1.
 template <bool TRANS, int KT, bool MULADD, bool MASK>
-__global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int ST) {
+SDTW_DEV void dist_bwd_tile(const DistBwdParams& p, int ST, int bx, int by, int b, int st,
+                            int ntx, int nty, int flag_id, DistBwdSmem& sm) {
     constexpr int KB = KT / 16;          // 16-wide feature blocks per wave
     constexpr int ZQ = BT * KT / 1024;   // 16-byte Z loads per thread per chunk
     static_assert(ZQ >= 1, "feature tile must feed 256 threads");
-    __shared__ __align__(16) float gbuf[2][GBUF];
-    __shared__ __align__(16) float zbuf[2][ZBUF];
-    __shared__ int last_piece;
-    // Workgroups are dispatched to the 8 XCDs round-robin by linear id; the id is remapped
-    // so that consecutive tiles (the row strips of one pair, which read the same Z) run on
-    // the same XCD and share its L2.
-    const int gx = gridDim.x, gy = gridDim.y;
-    const int nwg = gx * gy * gridDim.z;
-    const int id = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
-    const int v = (nwg & 7) == 0 ? (id & 7) * (nwg >> 3) + (id >> 3) : id;
-    // integer divisions expand to vector code: pin the (uniform) results to scalar registers
-    // so that the pipeline loop below is a uniform loop
-    const int bx = __builtin_amdgcn_readfirstlane(v % gx);
-    const int by = __builtin_amdgcn_readfirstlane((v / gx) % gy);
-    const int bz = __builtin_amdgcn_readfirstlane(v / (gx * gy));
-    const int b = __builtin_amdgcn_readfirstlane(bz / ST), st = bz - b * ST;
+    auto& gbuf = sm.gbuf;
+    auto& zbuf = sm.zbuf;
     const int r0 = by * 64;
     const int k0 = bx * KT;
     const int tid = threadIdx.x, l = tid & 63;
@@ -664,9 +661,12 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
         else if (fg) run(exact_tag, std::true_type{}, std::false_type{}, mk);
         else run(exact_tag, std::false_type{}, std::false_type{}, mk);
     };
-    // the gy pass: the mask is needed only if the gx pass saw a cost that was not positive
+    // the mask is needed only for a pair whose forward saw a cost that was not positive (where
+    // the forward recorded it), else, in the gy pass, only if the gx pass saw one
     bool use_mask = MASK;
-    if (MASK && TRANS && p.flags) {
+    if (MASK && p.clamped) {
+        use_mask = __builtin_amdgcn_readfirstlane(p.clamped[b]) != 0;
+    } else if (MASK && TRANS && p.flags) {
         int any = 0;
         for (int f = tid; f < p.nflags; f += 256) any |= p.flags[f];
         use_mask = __syncthreads_or(any);
@@ -684,7 +684,7 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
     } else {
         run_any(std::false_type{}, std::false_type{});
     }
-    if (MASK && !TRANS && p.flags && tid == 0) p.flags[id] = nonpos;
+    if (MASK && !TRANS && p.flags && flag_id >= 0 && tid == 0) p.flags[flag_id] = nonpos;
 
     // rs of row 16w + x: sum of the four lanes with (l & 15) == x
     float rs = rs_part + __shfl_xor(rs_part, 16);
@@ -703,8 +703,10 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
         }
     }
     if (ST > 1) {
-        const int64_t tile = ((int64_t)b * gy + by) * gx + bx;
-        float* part = p.part + tile * ST * 64 * KT;
+        // the passes' scratch regions are disjoint: gx first, then gy
+        const int64_t tile = ((int64_t)b * nty + by) * ntx + bx;
+        float* part = p.part + (TRANS ? dist_bwd_split_floats_x(p.B, p.N, p.M, p.K) : 0) + tile * ST * 64 * KT;
+        int* cnt = p.cnt + (TRANS ? dist_bwd_tiles(p.B, p.N, p.K) : 0);
         // partial of piece st: element (row 16w + 4(l>>4) + v, feature 16kb + (l&15))
         auto pidx = [&](int q, int v, int kb) {
             return ((int64_t)q * 64 + 16 * w + 4 * (l >> 4) + v) * KT + 16 * kb + (l & 15);
@@ -717,9 +719,9 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this thread's partials are stored
         __syncthreads();
         if (tid == 0)
-            last_piece = __hip_atomic_fetch_add(p.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ST - 1;
+            sm.last_piece = __hip_atomic_fetch_add(cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ST - 1;
         __syncthreads();
-        if (!last_piece) return;
+        if (!sm.last_piece) return;
 #pragma unroll
         for (int v = 0; v < 4; ++v)
 #pragma unroll
@@ -729,7 +731,7 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
                     sum += __hip_atomic_load(part + pidx(q, v, kb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 val[v][kb] = sum;
             }
-        if (tid == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_store(cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -740,6 +742,56 @@ __global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int
             const int k = k0 + 16 * kb + (l & 15);
             if (k < K) out[(int64_t)r * K + k] = 2.0f * val[v][kb];
         }
+    }
+}
+
+// One pass, grid (feature tiles, row strips, B * ST).  Workgroups are dispatched to the 8
+// XCDs round-robin by linear id; the id is remapped so that consecutive tiles (the row strips
+// of one pair, which read the same Z) run on the same XCD and share its L2.
+template <bool TRANS, int KT, bool MULADD, bool MASK>
+__global__ void __launch_bounds__(256) dist_bwd_mfma_kernel(DistBwdParams p, int ST) {
+    __shared__ __align__(16) DistBwdSmem sm;
+    const int ntx = gridDim.x, nty = gridDim.y;
+    const int nwg = ntx * nty * gridDim.z;
+    const int id = blockIdx.x + ntx * (blockIdx.y + nty * blockIdx.z);
+    const int v = (nwg & 7) == 0 ? (id & 7) * (nwg >> 3) + (id >> 3) : id;
+    // integer divisions expand to vector code: pin the (uniform) results to scalar registers
+    // so that the pipeline loop is a uniform loop
+    const int bx = __builtin_amdgcn_readfirstlane(v % ntx);
+    const int by = __builtin_amdgcn_readfirstlane((v / ntx) % nty);
+    const int bz = __builtin_amdgcn_readfirstlane(v / (ntx * nty));
+    const int b = __builtin_amdgcn_readfirstlane(bz / ST), st = bz - b * ST;
+    dist_bwd_tile<TRANS, KT, MULADD, MASK>(p, ST, bx, by, b, st, ntx, nty, id, sm);
+}
+
+// Both passes in one launch, tiles in pair-major order: pair b's gx tiles (STX pieces each),
+// then its gy tiles (STY pieces).  With the XCD remap of linear ids, a pair's tiles of both
+// passes run together on one XCD, so the pass that reads a G block second finds it in that
+// XCD's L2 (a pair's G, N*M*4 bytes, against 4 MiB of L2) rather than in HBM.  Used where the
+// gy pass does not wait on the gx pass's mask record: no mask, or per-pair clamp records
+// from the forward.
+template <int KT, bool MULADD, bool MASK>
+__global__ void __launch_bounds__(256) dist_bwd_merged_kernel(DistBwdParams p, int STX, int STY) {
+    __shared__ __align__(16) DistBwdSmem sm;
+    const int ntx = (p.K + KT - 1) / KT;
+    const int rx = (p.N + 63) / 64, ry = (p.M + 63) / 64;
+    const int tx = ntx * rx * STX, ty = ntx * ry * STY;  // tiles per pair of each pass
+    const int nwg = gridDim.x;
+    const int id = blockIdx.x;
+    const int v = (nwg & 7) == 0 ? (id & 7) * (nwg >> 3) + (id >> 3) : id;
+    const int b = __builtin_amdgcn_readfirstlane(v / (tx + ty));
+    const int k = __builtin_amdgcn_readfirstlane(v - b * (tx + ty));
+    if (k < tx) {
+        const int bx = __builtin_amdgcn_readfirstlane(k % ntx);
+        const int by = __builtin_amdgcn_readfirstlane((k / ntx) % rx);
+        const int st = __builtin_amdgcn_readfirstlane(k / (ntx * rx));
+        dist_bwd_tile<false, KT, MULADD, MASK>(p, STX, bx, by, b, st, ntx, rx, -1, sm);
+    } else {
+        const int kk = k - tx;
+        const int bx = __builtin_amdgcn_readfirstlane(kk % ntx);
+        const int by = __builtin_amdgcn_readfirstlane((kk / ntx) % ry);
+        const int st = __builtin_amdgcn_readfirstlane(kk / (ntx * ry));
+        dist_bwd_tile<true, KT, MULADD, MASK>(p, STY, bx, by, b, st, ntx, ry, -1, sm);
     }
 }
 
@@ -771,12 +823,45 @@ static void launch_dist_bwd_one(const DistBwdParams& p, hipStream_t st) {
     }
 }
 
+template <bool MULADD>
+static void launch_dist_bwd_merged(const DistBwdParams& p, hipStream_t st) {
+    const int KT = dist_bwd_kt(p.K);
+    const int STX = p.part ? dist_bwd_splits(p.B, p.N, p.M, p.K) : 1;
+    const int STY = p.part ? dist_bwd_splits(p.B, p.M, p.N, p.K) : 1;
+    const int64_t ntx = (p.K + KT - 1) / KT;
+    const int64_t tiles = (int64_t)p.B * ntx * (((p.N + 63) / 64) * STX + ((p.M + 63) / 64) * STY);
+    const dim3 grid((unsigned)tiles);
+    if (p.mask) {
+        if (KT == 16)
+            hipLaunchKernelGGL((dist_bwd_merged_kernel<16, MULADD, true>), grid, dim3(256), 0, st, p, STX, STY);
+        else if (KT == 32)
+            hipLaunchKernelGGL((dist_bwd_merged_kernel<32, MULADD, true>), grid, dim3(256), 0, st, p, STX, STY);
+        else
+            hipLaunchKernelGGL((dist_bwd_merged_kernel<64, MULADD, true>), grid, dim3(256), 0, st, p, STX, STY);
+    } else {
+        if (KT == 16)
+            hipLaunchKernelGGL((dist_bwd_merged_kernel<16, MULADD, false>), grid, dim3(256), 0, st, p, STX, STY);
+        else if (KT == 32)
+            hipLaunchKernelGGL((dist_bwd_merged_kernel<32, MULADD, false>), grid, dim3(256), 0, st, p, STX, STY);
+        else
+            hipLaunchKernelGGL((dist_bwd_merged_kernel<64, MULADD, false>), grid, dim3(256), 0, st, p, STX, STY);
+    }
+}
+
 hipError_t launch_dist_bwd(const DistBwdParams& p, hipStream_t st) {
     const bool split = p.part && (dist_bwd_splits(p.B, p.N, p.M, p.K) > 1 || dist_bwd_splits(p.B, p.M, p.N, p.K) > 1);
     if (split) {  // counters start at zero; every pass leaves them at zero
         const int64_t n = dist_bwd_counters(p.B, p.N, p.M, p.K);
         const int blocks = (int)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
         hipLaunchKernelGGL(zero_ints_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, st, p.cnt, n);
+    }
+    // both gradients, and no mask record to pass from the gx pass to the gy pass: one launch
+    if (p.gx && p.gy && (!p.mask || p.clamped)) {
+        DistBwdParams q = p;
+        q.flags = nullptr;
+        if (q.muladd) launch_dist_bwd_merged<true>(q, st);
+        else launch_dist_bwd_merged<false>(q, st);
+        return hipGetLastError();
     }
     // with the mask, the gx pass writes one flag per workgroup, which the gy pass reads; a
     // null gx or gy skips that pass (a gy pass without a gx pass applies the full mask)

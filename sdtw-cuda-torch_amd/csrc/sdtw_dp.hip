@@ -19,10 +19,12 @@ hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st) {
     const unsigned long long hi = bwd ? 0ull : kEmpty64;
     if (P.x2_fill) {  // with the fused recursions' row norms (and the gradient mode's zeroing)
         const int64_t ngy = bwd && P.gy_out ? (int64_t)P.B * P.M * P.K : 0;
+        const int64_t ncl = !bwd && P.D_out && P.clamped ? (int64_t)P.B : 0;
         return launch_prep_norms(P.ticket, P.err, reinterpret_cast<unsigned long long*>(P.gring),
                                  nwords, lo, hi, P.x, P.x2_fill, (int64_t)P.B * P.N, P.y,
                                  P.y2_fill, (int64_t)P.B * P.M, P.K,
-                                 reinterpret_cast<unsigned*>(P.gy_out), ngy, nullptr, 0, st);
+                                 reinterpret_cast<unsigned*>(P.gy_out), ngy,
+                                 reinterpret_cast<unsigned*>(P.clamped), ncl, st);
     }
     int64_t blocks = (nwords + 255) / 256;
     blocks = blocks < 1 ? 1 : (blocks > 2048 ? 2048 : blocks);

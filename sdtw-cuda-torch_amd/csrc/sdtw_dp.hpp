@@ -379,6 +379,7 @@ struct CostMfma {
     float yb[NKK];     // B: y[c0 + (l & 15)][4 kk + (l >> 4)]
     float y2n, y2c;    // norm of the issued / the begun tile's column
     bool tile_bad;     // the last finished tile holds a non-finite cost (wave-uniform)
+    bool tile_nonpos;  // ... a cost that is not positive (0 or NaN; wave-uniform)
     floatx4 acc[4];
     SDTW_DEV void init(const DPParams& P, int p, int b) {
         const int l = threadIdx.x & (WAVE - 1);
@@ -454,6 +455,7 @@ struct CostMfma {
         float* dst = ring + 4 * (l >> 4) * CS + sl;
         const bool mir = sl < U;  // the mirror slots
         float sum = 0.0f;
+        float mn = __builtin_inff();
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -462,8 +464,12 @@ struct CostMfma {
                 dst[(16 * rb + r) * CS] = v;
                 if (mir) dst[(16 * rb + r) * CS + CR] = v;
                 sum += v;
+                mn = (v > 0.0f) ? fminf(mn, v) : 0.0f;  // NaN or 0 -> 0
             }
         tile_bad = __builtin_amdgcn_ballot_w64(!(fabsf(sum) < __builtin_inff())) != 0;
+        // entries of rows >= N or columns >= M repeat the last row / column (clamped
+        // indices), so the tile holds a non-positive cost iff a cell of the table does
+        tile_nonpos = __builtin_amdgcn_ballot_w64(!(mn > 0.0f)) != 0;
     }
     // the same tile into the pair's cost tensor Dp (N, M): lane l's column c0 + (l & 15) of
     // rows row0 + 16 rb + 4 (l >> 4) + r, 16 lanes per 64-byte row segment
@@ -699,6 +705,7 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
     int* ready = sm.ready() + w;
     int known = 0;
     bool marked = false;  // the band's first non-finite cost tile has been published
+    bool clamp_marked = false;  // the pair's clamp record has been set by this wave
     const int groups = P.S / U;  // groups of the compute wave
     const int T = groups + 1;    // tiles it reads
     auto col = [&](int t) { return BWD ? P.M - TC * (t + 1) : TC * t; };
@@ -730,9 +737,15 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
         if ((threadIdx.x & (WAVE - 1)) == 0) lds_publish(ready, t + 1);
         if (t + 1 < T) c.issue(col(t + 1));
         // unfused mode's cost tensor, from the same tile (forward; after the next loads, so
-        // that they do not queue behind these stores)
+        // that they do not queue behind these stores), and the pair's clamp record
         if constexpr (MMA && !BWD) {
-            if (P.D_out) c.store_d(P.D_out + (int64_t)p * P.N * P.M, col(t), b * WAVE, P.N);
+            if (P.D_out) {
+                c.store_d(P.D_out + (int64_t)p * P.N * P.M, col(t), b * WAVE, P.N);
+                if (P.clamped && c.tile_nonpos && !clamp_marked) {
+                    clamp_marked = true;
+                    if ((threadIdx.x & (WAVE - 1)) == 0) P.clamped[p] = 1;
+                }
+            }
         }
         if (flush) gt.write(P, p, b);
     }

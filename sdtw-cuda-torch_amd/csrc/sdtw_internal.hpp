@@ -26,6 +26,9 @@ struct DPParams {
     float* gy_out;
     const float* gout;  // backward: (B) upstream gradient or nullptr (= 1)
     float* D_out;       // fused forward: the cost tiles also stored here (B,N,M), or nullptr
+    int* clamped;       // with D_out: per pair, set to 1 if a stored cost is not positive
+                        // (0 or NaN: the distance backward's clamp mask is then not the
+                        // identity); zeroed by the prep launch.  Or nullptr.
     float* x2_fill;     // fused: x2 / y2 (writable) for the prep launch to form, or nullptr
     float* y2_fill;
     int* ticket;        // workgroup ticket counter (zeroed by the prep kernel)
@@ -61,19 +64,21 @@ struct DistBwdParams {
     int mask;
     int muladd;
     float* part;      // split-reduction partials (dist_bwd_split_floats) or nullptr
-    int* cnt;         // per-tile arrival counters (dist_bwd_tiles ints), or nullptr
+    int* cnt;         // per-tile arrival counters (dist_bwd_counters ints), or nullptr
     int* flags;       // mask: per gx-pass workgroup "a cost was not positive" (dist_bwd_flags)
     int nflags;
+    const int* clamped;  // mask: per pair "a cost was not positive" from the forward, or
+                         // nullptr (unknown: the mask reads D)
 };
 
 // Split reduction of the distance backward: the reduction of a 64-row x KT-feature output
 // tile is cut into dist_bwd_splits() pieces (of whole 64-wide chunks) so that about 256
 // workgroups, one per CU, are in flight.
-inline int dist_bwd_kt(int64_t K) { return K <= 16 ? 16 : (K <= 32 ? 32 : 64); }
-inline int64_t dist_bwd_tiles(int64_t B, int64_t R, int64_t K) {
+__host__ __device__ inline int dist_bwd_kt(int64_t K) { return K <= 16 ? 16 : (K <= 32 ? 32 : 64); }
+__host__ __device__ inline int64_t dist_bwd_tiles(int64_t B, int64_t R, int64_t K) {
     return B * ((R + 63) / 64) * ((K + dist_bwd_kt(K) - 1) / dist_bwd_kt(K));
 }
-inline int dist_bwd_splits(int64_t B, int64_t R, int64_t T, int64_t K) {
+__host__ __device__ inline int dist_bwd_splits(int64_t B, int64_t R, int64_t T, int64_t K) {
     const int64_t tiles = dist_bwd_tiles(B, R, K);
     const int64_t chunks = (T + 63) / 64;
     int64_t st = (256 + tiles - 1) / tiles;
@@ -81,16 +86,17 @@ inline int dist_bwd_splits(int64_t B, int64_t R, int64_t T, int64_t K) {
     st = st > chunks ? chunks : st;
     return (int)(st < 1 ? 1 : st);
 }
-// scratch floats / counters for both passes (gx over N rows, gy over M rows), reused
-inline int64_t dist_bwd_split_floats(int64_t B, int64_t N, int64_t M, int64_t K) {
-    const int64_t kt = dist_bwd_kt(K);
-    const int64_t a = dist_bwd_tiles(B, N, K) * dist_bwd_splits(B, N, M, K);
-    const int64_t b = dist_bwd_tiles(B, M, K) * dist_bwd_splits(B, M, N, K);
-    return (a > b ? a : b) * 64 * kt;
+// scratch floats / counters of the two passes (gx over N rows first, then gy over M rows:
+// disjoint, since the passes may run in one launch)
+__host__ __device__ inline int64_t dist_bwd_split_floats_x(int64_t B, int64_t N, int64_t M, int64_t K) {
+    const int st = dist_bwd_splits(B, N, M, K);
+    return st > 1 ? dist_bwd_tiles(B, N, K) * st * 64 * dist_bwd_kt(K) : 0;  // unsplit: none
 }
-inline int64_t dist_bwd_counters(int64_t B, int64_t N, int64_t M, int64_t K) {
-    const int64_t a = dist_bwd_tiles(B, N, K), b = dist_bwd_tiles(B, M, K);
-    return a > b ? a : b;
+__host__ __device__ inline int64_t dist_bwd_split_floats(int64_t B, int64_t N, int64_t M, int64_t K) {
+    return dist_bwd_split_floats_x(B, N, M, K) + dist_bwd_split_floats_x(B, M, N, K);
+}
+__host__ __device__ inline int64_t dist_bwd_counters(int64_t B, int64_t N, int64_t M, int64_t K) {
+    return dist_bwd_tiles(B, N, K) + dist_bwd_tiles(B, M, K);
 }
 // workgroups of the gx pass (tiles times reduction pieces), one flag each
 inline int64_t dist_bwd_flags(int64_t B, int64_t N, int64_t M, int64_t K) {

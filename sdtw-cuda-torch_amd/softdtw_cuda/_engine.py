@@ -32,6 +32,7 @@ _SIGS = {
     "sdtw_get_numerics": ([], ctypes.c_int),
     "sdtw_set_wait_limit": ([ctypes.c_uint], ctypes.c_uint),
     "sdtw_set_deterministic": ([ctypes.c_int], ctypes.c_int),
+    "sdtw_dist_record_bytes": ([ctypes.c_int64] * 3, ctypes.c_size_t),
     "sdtw_fused_bands_per_workgroup": ([ctypes.c_int64] * 4, ctypes.c_int),
     "sdtw_workspace_bytes": ([ctypes.c_int] + [ctypes.c_int64] * 4, ctypes.c_size_t),
     "sdtw_table_elems": ([ctypes.c_int64] * 3, ctypes.c_int64),
@@ -41,7 +42,7 @@ _SIGS = {
     "sdtw_sqeuclid_fwd_f32": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 4
                               + [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                               ctypes.c_int),
-    "sdtw_sqeuclid_bwd_f32": ([ctypes.c_void_p] * 6 + [ctypes.c_int64] * 4
+    "sdtw_sqeuclid_bwd_f32": ([ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4
                               + [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                               ctypes.c_int),
     "sdtw_fwd_f32": ([ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3
@@ -56,7 +57,7 @@ _SIGS = {
     "sdtw_fused_fwd_f32": ([ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4
                            + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                            ctypes.c_int),
-    "sdtw_fused_fwd_d_f32": ([ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4
+    "sdtw_fused_fwd_d_f32": ([ctypes.c_void_p] * 6 + [ctypes.c_int64] * 4
                              + [ctypes.c_double] * 2 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
                              ctypes.c_int),
     "sdtw_fused_bwd_f32": ([ctypes.c_void_p] * 6 + [ctypes.c_int64] * 4
@@ -267,9 +268,11 @@ def sqeuclid_fwd(x: torch.Tensor, y: torch.Tensor, mode: int = DIST_EXACT) -> to
     return D
 
 
-def sqeuclid_bwd(x, y, D, G, mask: bool = True, need=(True, True)):
+def sqeuclid_bwd(x, y, D, G, mask: bool = True, need=(True, True), record=None):
     """(gx, gy) of the distance given G = dL/dD; an entry of `need` that is False skips that
-    gradient (returned as None)."""
+    gradient (returned as None).  record: the distance record fused_fwd_d wrote with D (per
+    pair clamp flags and row norms: pairs without a clamped cost skip reading D, and no norms
+    launch is needed), or None."""
     for t, n in ((x, "x"), (y, "y"), (G, "G")):
         require_gpu(t, f"sqeuclid backward {n}")
     if mask:
@@ -283,9 +286,10 @@ def sqeuclid_bwd(x, y, D, G, mask: bool = True, need=(True, True)):
     gy = torch.empty_like(y) if need[1] else None
     ws, nws = _workspace(OP_SQEUCLID_BWD, B, N, M, K, x.device)
     with torch.cuda.device(x.device):
-        rc = load().sdtw_sqeuclid_bwd_f32(_ptr(x), _ptr(y), _ptr(D if mask else None), _ptr(G),
-                                          _ptr(gx), _ptr(gy), B, N, M, K, 1 if mask else 0,
-                                          _ptr(ws), nws, _stream(x.device))
+        rc = load().sdtw_sqeuclid_bwd_f32(_ptr(x), _ptr(y), _ptr(D if mask else None),
+                                          _ptr(record if mask else None), _ptr(G), _ptr(gx),
+                                          _ptr(gy), B, N, M, K, 1 if mask else 0, _ptr(ws), nws,
+                                          _stream(x.device))
     _check(rc, "sqeuclid backward")
     return gx, gy
 
@@ -388,7 +392,9 @@ def one_launch_unfused_forward(B: int, N: int, M: int, K: int, device) -> bool:
 
 
 def fused_fwd_d(x, y, gamma: float, bandwidth: float):
-    """Unfused mode's forward in one launch: (out, R, D) with D the (B,N,M) cost tensor."""
+    """Unfused mode's forward in one launch: (out, R, D, record) with D the (B,N,M) cost
+    tensor and record its distance record for sqeuclid_bwd (uint8 device buffer: per-pair
+    int32 flags, 1 where a cost is not positive, then the row norms of x and y)."""
     require_gpu(x, "fused forward x")
     require_gpu(y, "fused forward y")
     _check_shapes(x=x, y=y)
@@ -397,14 +403,16 @@ def fused_fwd_d(x, y, gamma: float, bandwidth: float):
     D = torch.empty((B, N, M), dtype=torch.float32, device=x.device)
     R = torch.empty((table_elems(B, N, M),), dtype=torch.float32, device=x.device)
     out = torch.empty((B,), dtype=torch.float32, device=x.device)
+    record = torch.empty((int(load().sdtw_dist_record_bytes(B, N, M)),), dtype=torch.uint8,
+                         device=x.device)
     ws, nws = _workspace(OP_FUSED_FWD, B, N, M, K, x.device)
     with torch.cuda.device(x.device):
-        rc = load().sdtw_fused_fwd_d_f32(_ptr(x), _ptr(y), _ptr(D), _ptr(R), _ptr(out), B, N, M,
-                                         K, float(gamma), float(bandwidth), _ptr(ws), nws,
-                                         _stream(x.device))
+        rc = load().sdtw_fused_fwd_d_f32(_ptr(x), _ptr(y), _ptr(D), _ptr(record), _ptr(R),
+                                         _ptr(out), B, N, M, K, float(gamma), float(bandwidth),
+                                         _ptr(ws), nws, _stream(x.device))
     _check(rc, "fused forward (with D)")
     _debug_check(OP_FUSED_FWD, ws, nws, B, N, M, K, "fused forward (with D)")
-    return out, R, D
+    return out, R, D, record
 
 
 def fused_bwd(x, y, R, gamma: float, bandwidth: float, gout=None, need=(True, True)):

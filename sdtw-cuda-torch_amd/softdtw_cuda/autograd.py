@@ -57,8 +57,9 @@ class SoftDTWSqEuclidAutograd(Function):
     (the bits sdtw_sqeuclid_fwd_f32 writes, from the fused forward's matrix-core producer
     waves) and the recursion over it (sdtw_fused_fwd_d_f32).  The backward is the unfused
     chain: G = g * E over D (sdtw_bwd_f32), then the distance's chain rule with the clamp
-    mask (sdtw_sqeuclid_bwd_f32).  Same results as pairwise_distance followed by
-    SoftDTWAutograd (reference distances.py:6-28, autograd.py:11-48)."""
+    mask (sdtw_sqeuclid_bwd_f32), which skips D for the pairs the forward recorded as free of
+    clamped costs and takes the row norms the forward formed.  Same results as pairwise_distance followed by SoftDTWAutograd (reference
+    distances.py:6-28, autograd.py:11-48)."""
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, y: torch.Tensor, gamma: float, bandwidth: float | None):
@@ -66,16 +67,17 @@ class SoftDTWSqEuclidAutograd(Function):
         if gamma_f <= 0:
             raise ValueError(f"gamma must be > 0, got {gamma_f}")
         bandwidth_f = _normalize_bandwidth(bandwidth)
-        out, R, D = _engine.fused_fwd_d(x, y, gamma_f, bandwidth_f)
-        ctx.save_for_backward(x, y, D, R)
+        out, R, D, record = _engine.fused_fwd_d(x, y, gamma_f, bandwidth_f)
+        ctx.save_for_backward(x, y, D, R, record)
         ctx.gamma = gamma_f
         ctx.bandwidth = bandwidth_f
         return out
 
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor):
-        x, y, D, R = ctx.saved_tensors
+        x, y, D, R, record = ctx.saved_tensors
         g = grad_output.reshape(-1).to(device=D.device, dtype=torch.float32).contiguous()
         G = _engine.dtw_bwd(D, R, ctx.gamma, ctx.bandwidth, gout=g)
-        gx, gy = _engine.sqeuclid_bwd(x, y, D, G, mask=True, need=ctx.needs_input_grad[:2])
+        gx, gy = _engine.sqeuclid_bwd(x, y, D, G, mask=True, need=ctx.needs_input_grad[:2],
+                                      record=record)
         return gx, gy, None, None

@@ -198,8 +198,19 @@ def test_unfused_one_launch_forward_matches_two_calls(B, N, M, K, bw):
     xg, yg = x.cuda(), y.cuda()
     D1 = _engine.sqeuclid_fwd(xg, yg)
     o1, R1 = _engine.dtw_fwd(D1, 0.7, bw)
-    o2, R2, D2 = _engine.fused_fwd_d(xg, yg, 0.7, bw)
+    o2, R2, D2, rec = _engine.fused_fwd_d(xg, yg, 0.7, bw)
     assert torch.equal(D1, D2) and torch.equal(R1, R2) and torch.equal(o1, o2)
+    # the distance record: per pair 1 exactly where it holds a cost that is not positive,
+    # then the row norms (256-byte aligned parts) with the norms kernel's bits
+    cl = rec[:4 * B].view(torch.int32)
+    want = (~(D1 > 0)).flatten(1).any(dim=1).to(torch.int32)
+    assert torch.equal(cl, want)
+    up = lambda n: (n + 255) // 256 * 256
+    x2 = rec[up(4 * B):up(4 * B) + 4 * B * N].view(torch.float32)
+    y2 = rec[up(4 * B) + up(4 * B * N):up(4 * B) + up(4 * B * N) + 4 * B * M].view(torch.float32)
+    # the row norms of the reference's op sequence (oracle.sqeuclidean: (x * x).sum(-1))
+    assert torch.equal(x2.cpu(), (x * x).sum(dim=-1).flatten())
+    assert torch.equal(y2.cpu(), (y * y).sum(dim=-1).flatten())
 
 
 @pytest.mark.parametrize("bandwidth", [None, 15.0])
