@@ -76,6 +76,7 @@ def algorithmic_bytes(kernel, B, N, M, K):
         "fused_fwd": 4 * (cells + xy),         # read x, y; write R
         "fused_fwd_d": 4 * (2 * cells + xy),   # read x, y; write D, R
         "fused_bwd_e": 4 * (2 * cells + xy),   # read R, x, y; write g*E
+        "fused_bwd": 4 * (cells + 2 * xy),     # read R, x, y; write gx, gy (no E)
     }[kernel]
 
 
@@ -111,6 +112,7 @@ def kernel_launcher(name, xg, yg, gamma):
         "fused_fwd": lambda: _engine.fused_fwd(xg, yg, gamma, -1.0),
         "fused_fwd_d": lambda: _engine.fused_fwd_d(xg, yg, gamma, -1.0),
         "fused_bwd_e": lambda: _engine.fused_bwd_e(xg, yg, R, gamma, -1.0),
+        "fused_bwd": lambda: _engine.fused_bwd(xg, yg, R, gamma, -1.0),
     }[name]
     return fn
 
@@ -360,7 +362,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel", default=None,
                     help="only launch one kernel family repeatedly (for rocprofv3 runs): "
-                         "dist_fwd, dp_fwd, dp_bwd, dist_bwd, fused_fwd, fused_fwd_d, fused_bwd_e, copy")
+                         "dist_fwd, dp_fwd, dp_bwd, dist_bwd, fused_fwd, fused_fwd_d, fused_bwd, "
+                         "fused_bwd_e, copy")
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--shape", default=None,
                     help="B,N,M,D for --kernel runs (default: the headline 32,512,512,64)")
@@ -443,14 +446,14 @@ def main(argv=None):
     if "unfused" in res:
         kernels += unfused_kernels
     if "fused" in res:
-        kernels += ["fused_fwd", "fused_bwd_e"]
+        kernels += ["fused_fwd", "fused_bwd"]
     per = {}
     for kname in kernels:
         fn = kernel_launcher(kname, X, Y, gamma)
         per[kname] = time_kernel(fn, max(5, min(args.steps, 20)))
         log(f"[bench] kernel {kname}: {per[kname]:.4f} ms/launch")
     head_mode = "unfused" if "unfused" in res else "fused"
-    head_kernels = {"unfused": unfused_kernels, "fused": ["fused_fwd", "fused_bwd_e"]}[head_mode]
+    head_kernels = {"unfused": unfused_kernels, "fused": ["fused_fwd", "fused_bwd"]}[head_mode]
     dom = max(head_kernels, key=per.get)  # dominant kernel of the step `value` measures
     abytes = algorithmic_bytes(dom, B, N, M, K)
     achieved = abytes / (per[dom] * 1e-3) / 1e9
