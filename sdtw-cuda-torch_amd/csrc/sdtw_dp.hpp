@@ -591,18 +591,19 @@ struct CostRing {
     }
 };
 
-// shared-memory layout of the DP kernels:
-//   [ticket, counters 256 B][exp (/ log) tables][handoff rings][cost rings]
-// W + 1 produced/consumed counter pairs, one per handoff ring; the tables are the exp table
-// (fm::kExpTabN doubles, 2 KiB), then, in the forward only, the log table (2 fm::kLogTabN
-// doubles, 8 KiB)
+// shared-memory layout of the DP kernels: static, the exp (/ log) tables at LDS address 0
+// (the exp table, fm::kExpTabN doubles, 2 KiB, then, in the forward only, the log table,
+// 2 fm::kLogTabN doubles, 8 KiB), so the cells' table reads fold the base into their
+// immediate offset; dynamic, [ticket, counters 256 B][handoff rings][cost rings], with
+// W + 1 produced/consumed counter pairs, one per handoff ring
 constexpr int kTabBytesFwd = (fm::kExpTabN + 2 * fm::kLogTabN) * 8;
 constexpr int kTabBytesBwd = fm::kExpTabN * 8;
 struct Smem {
-    unsigned char* base;
+    unsigned char* base;  // dynamic LDS
     int W;
     size_t ring_bytes;  // handoff rings of all bands
     int tab_bytes;      // kTabBytesFwd or kTabBytesBwd
+    double* tab;        // the kernel's static table array
     SDTW_DEV int* ticket() const { return reinterpret_cast<int*>(base); }
     SDTW_DEV int* prod() const { return reinterpret_cast<int*>(base) + 4; }
     SDTW_DEV int* cons() const { return reinterpret_cast<int*>(base) + 4 + (W + 1); }
@@ -618,10 +619,10 @@ struct Smem {
     // backward, gradient mode: G tiles copied out of the band's cost ring by its gradient
     // waves, for dL/dx (ints 48 .. 51) and for dL/dy (ints 52 .. 55)
     SDTW_DEV int* gdone() const { return reinterpret_cast<int*>(base) + 48; }
-    SDTW_DEV double* tables() const { return reinterpret_cast<double*>(base + 256); }
-    SDTW_DEV unsigned char* ring() const { return base + 256 + tab_bytes; }
+    SDTW_DEV double* tables() const { return tab; }
+    SDTW_DEV unsigned char* ring() const { return base + 256; }
     SDTW_DEV float* cost_ring(int w) const {
-        return reinterpret_cast<float*>(base + 256 + tab_bytes + ring_bytes) + (size_t)w * WAVE * CS;
+        return reinterpret_cast<float*>(base + 256 + ring_bytes) + (size_t)w * WAVE * CS;
     }
     // every thread of the workgroup, before the first barrier
     SDTW_DEV void load_tables() const {
@@ -1249,7 +1250,8 @@ constexpr int dp_threads() { return Produced<Cost, BWD>::value ? 9 * WAVE : 5 * 
 template <class Cost, bool BAND, bool EXACT>
 __global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W), kTabBytesFwd};
+    __shared__ __align__(16) double tab[kTabBytesFwd / 8];
+    Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W), kTabBytesFwd, tab};
     // wave-uniform values are moved to scalar registers so that the branches on band,
     // group and pair compile to scalar branches, not exec-masked regions
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -1517,7 +1519,8 @@ __global__ void __launch_bounds__((GW ? (grad_waves_per_band<GW>() * GW + 1) * W
 bwd_kernel(DPParams P) {
     static_assert(GW == 0 || KXOf<Cost>::value > 0, "gradient mode needs matrix-core cost tiles");
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W), kTabBytesBwd};
+    __shared__ __align__(16) double tab[kTabBytesBwd / 8];
+    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W), kTabBytesBwd, tab};
     // wave-uniform values are moved to scalar registers so that the branches on band,
     // group and pair compile to scalar branches, not exec-masked regions
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -1578,7 +1581,7 @@ hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st);
 
 inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
     const size_t ring = bwd ? ring_bytes_bwd(P.W) : ring_bytes_fwd(P.W);
-    return 256 + (bwd ? kTabBytesBwd : kTabBytesFwd) + ring + (size_t)P.W * WAVE * CS * sizeof(float);
+    return 256 + ring + (size_t)P.W * WAVE * CS * sizeof(float);  // the tables are static
 }
 
 template <class K>
