@@ -59,12 +59,6 @@ SDTW_DEV double shr1(double old, double v) {
     const int hi = dpp_shr1(__double2hiint(old), __double2hiint(v));
     return __hiloint2double(hi, lo);
 }
-// lane l receives lane l+1's v; lane 63 receives `old`
-SDTW_DEV double shl1(double old, double v) {
-    const int lo = dpp_shl1(__double2loint(old), __double2loint(v));
-    const int hi = dpp_shl1(__double2hiint(old), __double2hiint(v));
-    return __hiloint2double(hi, lo);
-}
 
 // LDS counters: relaxed accesses.  All LDS operations of a CU are performed as wave-wide
 // operations in one global order, a wave's in issue order, so a counter stored after ring
@@ -211,19 +205,26 @@ SDTW_DEV double fwd_cell_exact(double R0, double R1, double R2, float d, double 
     return fma(-gamma, fm::log_tab_1to3(rsum, L), ((double)d + m) + nanfix);
 }
 
-// fwd_cell_exact for finite inputs with a finite minimum, in fewer instructions: the minimum,
-// median and maximum of the predecessors come from a min/max network (the sum of the two
-// non-minimum terms does not depend on their order), and no NaN is restored.  Where those
+// fwd_cell_exact for finite inputs with a finite minimum, in fewer instructions: the minimum
+// and the two other predecessors come from a four-operation min/max network (lo, hi of the
+// diagonal and left ones; the minimum is min(lo, up), the others hi and max(lo, up); the sum
+// of the two non-minimum terms does not depend on their order), and no NaN is restored.  Where those
 // conditions hold it returns fwd_cell_exact's bits.  The forward takes it only while every
 // cost the band uses and every value the band above hands over is finite; then each active
 // cell has a finite predecessor (the diagonal one, or the left one in row 0, or R[0,0]).
 SDTW_DEV double fwd_cell_exact_finite(double R0, double R1, double R2, float d, double gamma,
                                       double inv_gamma, const double* T, const double* L) {
     const double lo = fmin(R0, R2), hi = fmax(R0, R2);
-    const double m = fmin(lo, R1), mx = fmax(hi, R1), md = fmax(lo, fmin(hi, R1));
-    const double ea = fm::exp_tab_abs((m - md) * inv_gamma, T);
-    const double eb = fm::exp_tab_abs((m - mx) * inv_gamma, T);
-    const double rsum = (ea + eb) + 1.0;
+    const double m = fmin(lo, R1), o = fmax(lo, R1);
+    const double xa = fm::exp_tab_abs_arg((m - o) * inv_gamma);
+    const double xb = fm::exp_tab_abs_arg((m - hi) * inv_gamma);
+    const double tca = fm::exp_tab_abs_tc(xa), tcb = fm::exp_tab_abs_tc(xb);
+    // (table reads written first; the compiler's own schedule measured faster than one
+    // pinned with scheduling barriers that waits for both after the polynomials)
+    const double fa = T[fm::lo_word(tca) & (fm::kExpTabN - 1)];
+    const double fb = T[fm::lo_word(tcb) & (fm::kExpTabN - 1)];
+    const double pa = fm::exp_tab_abs_em1(xa, tca), pb = fm::exp_tab_abs_em1(xb, tcb);
+    const double rsum = (fm::exp_tab_abs_join(fa, pa, tca) + fm::exp_tab_abs_join(fb, pb, tcb)) + 1.0;
     return fma(-gamma, fm::log_tab_1to3(rsum, L), (double)d + m);
 }
 
@@ -592,7 +593,8 @@ struct CostRing {
 };
 
 // shared-memory layout of the DP kernels: static, the exp (/ log) tables at LDS address 0
-// (the exp table, fm::kExpTabN doubles, 2 KiB, then, in the forward only, the log table,
+// (the exp table, fm::kExpTabN doubles, 2 KiB: kExp2Tab for the backward's exp_tab, its
+// folded form for the forward's exp_tab_abs; then, in the forward only, the log table,
 // 2 fm::kLogTabN doubles, 8 KiB), so the cells' table reads fold the base into their
 // immediate offset; dynamic, [ticket, counters 256 B][handoff rings][cost rings], with
 // W + 1 produced/consumed counter pairs, one per handoff ring
@@ -628,7 +630,9 @@ struct Smem {
     SDTW_DEV void load_tables() const {
         double* t = tables();
         for (int e = threadIdx.x; e < tab_bytes / 8; e += blockDim.x)
-            t[e] = e < fm::kExpTabN ? fm::kExp2Tab[e] : fm::kLogTab[e - fm::kExpTabN];
+            t[e] = e >= fm::kExpTabN  ? fm::kLogTab[e - fm::kExpTabN]
+                   : tab_bytes == kTabBytesFwd ? fm::exp2tab_folded(e)  // the forward's exp_tab_abs
+                                               : fm::kExp2Tab[e];
     }
 };
 
@@ -974,7 +978,10 @@ SDTW_DEV void grad_wave(const DPParams& P, const Smem& sm, int p, int b, int w) 
 }
 
 // W + 1 handoff rings: one per band plus the helper wave's
-SDTW_HD size_t ring_bytes_fwd(int W) { return (size_t)(W + 1) * RS * sizeof(double); }
+// (forward: then the workgroup's staging block of kStageFwd doubles, see fwd_band; at W = 4
+// it fills the 160 KiB of LDS exactly)
+constexpr int kStageFwd = WAVE + 2 * U;
+SDTW_HD size_t ring_bytes_fwd(int W) { return ((size_t)(W + 1) * RS + kStageFwd) * sizeof(double); }
 SDTW_HD size_t ring_bytes_bwd(int W) { return (size_t)(W + 1) * RS * sizeof(float4); }
 
 // ---------------------------------------------------------------------------------------
@@ -1006,6 +1013,14 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const double* lin = lring + w * RS;
     double* lout = lring + (w + 1) * RS;
     const int* lin_flag = sm.prod() + w;
+    // Last row to the band below: at every step each lane stores its value with one wide LDS
+    // write, so no cross-lane moves collect lane 63's values.  Lane 63's store (column
+    // s0 + u - 63 at step s0 + u) goes to the handoff ring, or, for the band that hands over
+    // through global memory (the workgroup's last, w = W - 1), to entries WAVE + U ..
+    // WAVE + 2U - 1 of the workgroup's staging block.  Every other store (lane l < 63, and
+    // lane 63 of a pair's last band) goes to entry l + u of the block's first WAVE + U
+    // entries, which all waves share and nothing reads.
+    double* stage = lring + (W + 1) * RS;
 
     float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
 
@@ -1016,10 +1031,6 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     double prev = INF;   // this lane's value one step ago (sent to lane l+1 by DPP)
 
     double up_cur[U];
-    // lane 63's value of each step, shifted one lane down per step: after the group's last
-    // step lane 63 - U + 1 + u holds the value of step u, so the handover is one wide write
-    // (or one global store) instead of U single-lane ones
-    double cap = INF;
     float d_cur[U], d_nxt[U];
 
     // Band above: columns [c0, c0 + U) of its last row from the LDS ring, for lane 0.  The
@@ -1056,19 +1067,25 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         if (live && l == 0) lds_publish(sm.cons() + w, need);
         return true;
     };
+    // Where this lane's per-step store of the group at s0 goes (entry u for step u).  Lane
+    // 63's ring stores are unconditional: slots of columns < 0 or >= M are never read before
+    // being rewritten or at all.
+    auto step_dst = [&](int s0) -> double* {
+        if (l == WAVE - 1 && out_lds) return lout + hslot(s0 - (WAVE - 1));
+        if (l == WAVE - 1 && out_glb) return stage + (WAVE + U);
+        return stage + l;
+    };
     // Hand the last row's columns computed by the group at s0 (lane 63 computed column
-    // s0 + u - 63 at step s0 + u) to the band below.  The LDS writes are unconditional:
-    // slots of columns < 0 or >= M are never read before being rewritten or at all.
+    // s0 + u - 63 at step s0 + u) to the band below: publish the ring entries lane 63 stored,
+    // or copy the staged ones to the cross-workgroup row.
     auto handover = [&](int s0) {
-        if (l < WAVE - U) return;
         const int c0 = s0 - (WAVE - 1);
-        const int u = l - (WAVE - U);  // step of the value this lane holds
         if (out_lds) {
-            lout[hslot(c0) + u] = cap;
             if (l == WAVE - 1) lds_publish(sm.prod() + (w + 1), min(max(s0 + U - (WAVE - 1), 0), M));
-        } else {
+        } else if (l >= WAVE - U) {
+            const int u = l - (WAVE - U);
             // columns in [-63, M + 15]: inside the row's padding, no test needed
-            glb_put(gout + c0 + u, cap);
+            glb_put(gout + c0 + u, stage[WAVE + U + u]);
         }
     };
 
@@ -1124,6 +1141,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
                 return -1;
         }
         float* Rg = Rt + (int64_t)s0 * WAVE;
+        double* dst = step_dst(s0);
         const float* dn = crow + ((s0 + TC - l) & (CR - 1));  // next group's costs
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -1151,7 +1169,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             left = r;
             diag = up;
             prev = r;
-            cap = shl1(r, cap);
+            dst[u] = r;
             Rg[u * WAVE] = (float)r;
             // next group's costs, and the tile work, between the steps
             d_nxt[u] = dn[u];

@@ -21,6 +21,8 @@ HARNESS = r"""
 #include "sdtw_math.hpp"
 using namespace sdtw::fm;
 int main() {
+    double Tf[kExpTabN];  // the forward's table for exp_tab_abs
+    for (int j = 0; j < kExpTabN; ++j) Tf[j] = exp2tab_folded(j);
     std::mt19937_64 g(12345);
     std::uniform_real_distribution<double> u01(0.0, 1.0);
     double emax = 0.0, amax = 0.0, lmax = 0.0;
@@ -33,7 +35,7 @@ int main() {
             if (err > emax) emax = err;
         }
         // the forward's variant: absolute accuracy (its result is added to 1)
-        const double aerr = (double)fabsl((long double)exp_tab_abs(x, kExp2Tab) - ref);
+        const double aerr = (double)fabsl((long double)exp_tab_abs(x, Tf) - ref);
         if (aerr > amax) amax = aerr;
         // log arguments: a soft-min's sum of exponentials, in [1, 3]
         const double s = 1.0 + 2.0 * u01(g);
@@ -45,8 +47,12 @@ int main() {
                 log_tab_1to3(1.0, kLogTab), log_tab_1to3(3.0, kLogTab));
     std::printf("%d %d\n", (int)std::isnan(log_tab_1to3(NAN, kLogTab)),
                 (int)(exp_tab(-1e300, kExp2Tab) == 0.0));
-    std::printf("%a %a %d\n", exp_tab_abs(0.0, kExp2Tab), exp_tab_abs(-INFINITY, kExp2Tab),
-                (int)(exp_tab_abs(-1e300, kExp2Tab) == 0.0));
+    // below the clamp: exp(-708), normal, and nothing next to 1
+    const double lo = exp_tab_abs(-708.0, Tf);
+    std::printf("%a %d %d\n", exp_tab_abs(0.0, Tf),
+                (int)(exp_tab_abs(-INFINITY, Tf) == lo && exp_tab_abs(-1e300, Tf) == lo &&
+                      exp_tab_abs(-750.0, Tf) == lo),
+                (int)(lo > 0x1p-1022 && lo < 0x1p-1020 && 1.0 + lo == 1.0 && 0.25 + lo == 0.25));
     return 0;
 }
 """
@@ -82,8 +88,11 @@ def test_special_values(harness_output):
     assert abs(l3 - 1.0986122886681098) < 4e-16
     nan_ok, tiny_ok = (int(v) for v in harness_output[2].split())
     assert nan_ok == 1 and tiny_ok == 1
-    a0, ainf, atiny = harness_output[3].split()
-    assert float.fromhex(a0) == 1.0 and float.fromhex(ainf) == 0.0 and int(atiny) == 1
+    # the forward's exp_tab_abs: exactly 1 at 0; every argument below -708 (and -inf, for
+    # +inf predecessors) gives exp(-708), a normal number that vanishes next to 1 and to any
+    # other term of the soft-min's sum, as 0 would
+    a0, aclamp, avanish = harness_output[3].split()
+    assert float.fromhex(a0) == 1.0 and int(aclamp) == 1 and int(avanish) == 1
 
 
 def test_tables_are_generated_from_the_committed_generator():
