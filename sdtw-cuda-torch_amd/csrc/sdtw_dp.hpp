@@ -982,7 +982,9 @@ SDTW_DEV void grad_wave(const DPParams& P, const Smem& sm, int p, int b, int w) 
 // it fills the 160 KiB of LDS exactly)
 constexpr int kStageFwd = WAVE + 2 * U;
 SDTW_HD size_t ring_bytes_fwd(int W) { return ((size_t)(W + 1) * RS + kStageFwd) * sizeof(double); }
-SDTW_HD size_t ring_bytes_bwd(int W) { return (size_t)(W + 1) * RS * sizeof(float4); }
+// (backward: then the workgroup's staging block of kStageBwd bytes, see bwd_band)
+constexpr int kStageBwd = 12 * WAVE + 16 * U + 16 * U;
+SDTW_HD size_t ring_bytes_bwd(int W) { return (size_t)(W + 1) * RS * sizeof(float4) + kStageBwd; }
 
 // ---------------------------------------------------------------------------------------
 // Forward
@@ -1352,6 +1354,17 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const float4* lin = lring + (w + 1) * RS;
     float4* lout = lring + w * RS;
     const int* lin_flag = sm.prod() + (w + 1);
+    // First row to the band above: at every step each lane stores its (E, R, D) with two LDS
+    // writes (E and R by one two-address write, D), so no cross-lane moves collect lane 0's
+    // values.  Lane 0's stores (sequence number q - 63 at reverse step q) go to the x, y, z
+    // of the handoff ring's entries (w is not read), or, for the band that hands over
+    // through global memory (the workgroup's first, w = 0), to the last U float4 entries of
+    // the workgroup's staging block.  Every other store (lanes 1 .. 63, and lane 0 of a
+    // pair's first band) goes to bytes 12 l + 16 u .. + 11 of the block's first part, which
+    // all waves share and nothing reads (a stride of three words between lanes keeps each
+    // write free of bank conflicts).
+    unsigned char* stage = sm.ring() + (size_t)(W + 1) * RS * sizeof(float4);
+    float4* stage_glb = reinterpret_cast<float4*>(stage + 12 * WAVE + 16 * U);
 
     const float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
 
@@ -1363,10 +1376,6 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     float pE = 0.0f, pR = NINF, pD = 0.0f;  // published one step ago
 
     float4 dn_cur[U];
-    // lane 0's (E, R, D) of each step, shifted one lane up per step: after the group's last
-    // step lane k (< U) holds the entry of step U - 1 - k, so the handover is one wide write
-    // (or one pair of global stores) instead of U single-lane ones
-    float capE = 0.0f, capR = 0.0f, capD = 0.0f;
     float r_cur[U], r_nxt[U], d_cur[U], d_nxt[U];
     // Band below: sequence numbers [q0, q0 + U) of its first row from the LDS ring, for
     // lane 63.  Where no band lies below, the values are the padding row below the table
@@ -1385,18 +1394,23 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         if (l == 0) lds_publish(sm.cons() + (w + 1), need);
         return true;
     };
+    // where this lane's per-step stores of the group at q0 go (float4 entry u for step u,
+    // x y z written); lane 0's ring stores are unconditional, as in the forward
+    auto step_dst = [&](int q0) -> float* {
+        if (l == 0 && out_lds) return reinterpret_cast<float*>(lout + hslot(q0 - (WAVE - 1)));
+        if (l == 0 && out_glb) return reinterpret_cast<float*>(stage_glb);
+        return reinterpret_cast<float*>(stage + 12 * l);
+    };
     // hand the band's first row to the band above: lane 0 produced sequence numbers
-    // q - 63 (= M - 1 - j) during the group at q0, now held by lanes 0 .. U - 1 (LDS writes
-    // unconditional, as in the forward; the count is published after them)
+    // q - 63 (= M - 1 - j) during the group at q0; publish the ring entries it stored (the
+    // count after them), or copy the staged ones to the cross-workgroup row
     auto handover = [&](int q0) {
-        if (l >= U) return;
         const int c0 = q0 - (WAVE - 1);
-        const float4 v = make_float4(capE, capR, capD, 1.0f);
         if (out_lds) {
-            lout[hslot(c0) + (U - 1 - l)] = v;
             if (l == 0) lds_publish(sm.prod() + w, min(max(q0 + U - (WAVE - 1), 0), M));
-        } else {
-            glb_put4(gout + c0 + (U - 1 - l), v);
+        } else if (l < U) {
+            const float4 v = stage_glb[l];
+            glb_put4(gout + c0 + l, make_float4(v.x, v.y, v.z, 1.0f));
         }
     };
     // Each step writes g*E of the lane's cell into the cost-ring slot whose cost it has just
@@ -1455,6 +1469,12 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             if (need_free > 0 && !wait_at_least(sm.cons() + w, need_free, known_free, P.err, P.spin_limit))
                 return false;
         }
+        float* dst = step_dst(q0);
+        // next group's costs: columns (M + 62 - l) - n0 - u, U consecutive slots from the
+        // lowest one (mirrored past CR), read downwards; next group's R: in an interior group
+        // every forward step M + 62 - n0 - u is >= 0, so no clamp
+        const float* dnx = crow + ((M + 62 - l - n0 - (U - 1)) & (CR - 1));
+        const float* rnx = Rt + (int64_t)(M + 62 - n0) * WAVE;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int q = q0 + u;
@@ -1491,13 +1511,13 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             pE = mE;
             pR = mR;
             pD = mD;
-            capE = __int_as_float(dpp_shr1(__float_as_int(mE), __float_as_int(capE)));
-            capR = __int_as_float(dpp_shr1(__float_as_int(mR), __float_as_int(capR)));
-            capD = __int_as_float(dpp_shr1(__float_as_int(mD), __float_as_int(capD)));
+            dst[4 * u] = mE;
+            dst[4 * u + 1] = mR;
+            dst[4 * u + 2] = mD;
             // next group's R and costs, and the tile work, between the steps (fstep clamps
             // reads past the band's first step)
-            r_nxt[u] = Rt[(int64_t)fstep(n0 + u) * WAVE];
-            d_nxt[u] = crow[ring_col(n0 + u)];
+            r_nxt[u] = INTERIOR ? rnx[-(int64_t)u * WAVE] : Rt[(int64_t)fstep(n0 + u) * WAVE];
+            d_nxt[u] = dnx[U - 1 - u];
             cost.step(u, tile_col(q0 + 2 * TC), tile_col(q0 + 3 * TC));
         }
         cost.end(cring, tile_col(q0 + 2 * TC), tile_col(q0 + 3 * TC));
