@@ -89,8 +89,16 @@ int fused_wmax(int64_t B, int64_t N, int64_t M, int64_t K) {
     if (!mfma_costs(N, M, K)) return 4;
     return B * dp_geom(N, 2).G <= cu_count() ? 2 : 4;
 }
-// workspace sizing: the 2-band geometry needs the most cross-workgroup rows
-int fused_ws_wmax(int64_t N, int64_t M, int64_t K) { return mfma_costs(N, M, K) ? 2 : 4; }
+// The fused backward: one band per workgroup when the batch's one-band workgroups all fit
+// on the GPU at once.  Its producer wave (matrix-core cost tiles) and, in gradient mode, its
+// dL/dx and dL/dy waves (matrix-core products with the E tiles) then each have a SIMD and its
+// matrix core to themselves; at two bands per workgroup two of these waves share one.
+int fused_bwd_wmax(int64_t B, int64_t N, int64_t M, int64_t K) {
+    if (mfma_costs(N, M, K) && B * dp_geom(N, 1).G <= cu_count()) return 1;
+    return fused_wmax(B, N, M, K);
+}
+// workspace sizing: the 1-band geometry needs the most cross-workgroup rows
+int fused_ws_wmax(int64_t N, int64_t M, int64_t K) { return mfma_costs(N, M, K) ? 1 : 4; }
 // Process-wide: whether the fused backward must give run-to-run identical bits
 // (sdtw_set_deterministic).
 std::atomic<int> g_deterministic{0};
@@ -104,7 +112,7 @@ std::atomic<int> g_deterministic{0};
 bool fused_grad_mode(int64_t B, int64_t N, int64_t M, int64_t K, bool forms_gy = true) {
     if (forms_gy && g_deterministic.load(std::memory_order_relaxed)) return false;
     if (!mfma_costs(N, M, K)) return false;
-    return fused_wmax(B, N, M, K) <= 2 || K <= 16;
+    return fused_bwd_wmax(B, N, M, K) <= 2 || K <= 16;
 }
 
 // distance-backward split-reduction scratch: partials, then counters
@@ -498,7 +506,7 @@ static int fused_bwd_common(const float* x, const float* y, const float* R, cons
                             int64_t N, int64_t M, int64_t K, double gamma, double bandwidth,
                             hipStream_t st) {
     DPParams p{};
-    fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_wmax(B, N, M, K));
+    fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_bwd_wmax(B, N, M, K));
     p.x = x;
     p.y = y;
     p.x2 = x2;
@@ -522,13 +530,13 @@ int sdtw_fused_bwd_f32(const float* x, const float* y, const float* R, const flo
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const DPScratch d = carve_dp(c, B, N, M, fused_wmax(B, N, M, K));
+    const DPScratch d = carve_dp(c, B, N, M, fused_bwd_wmax(B, N, M, K));
     if (fused_grad_mode(B, N, M, K, gy != nullptr)) {
         // the gradients inside the recursion kernel: dL/dy is zeroed by the prep launch and
         // accumulated band by band, dL/dx written per band
         if (!c.ok) return SDTW_ERR_WORKSPACE;
         DPParams p{};
-        fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_wmax(B, N, M, K));
+        fill_dp(p, d, B, N, M, K, gamma, bandwidth, fused_bwd_wmax(B, N, M, K));
         p.x = x;
         p.y = y;
         p.x2 = x2;
@@ -575,7 +583,7 @@ int sdtw_fused_bwd_e_f32(const float* x, const float* y, const float* R, const f
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const DPScratch d = carve_dp(c, B, N, M, fused_wmax(B, N, M, K));
+    const DPScratch d = carve_dp(c, B, N, M, fused_bwd_wmax(B, N, M, K));
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     return fused_bwd_common(x, y, R, gout, E, x2, y2, d, B, N, M, K, gamma, bandwidth,
                             (hipStream_t)stream);

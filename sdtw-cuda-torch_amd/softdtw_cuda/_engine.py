@@ -373,8 +373,8 @@ def fused_costs_on_matrix_cores(N: int, M: int, K: int) -> bool:
 
 
 def fused_bands_per_workgroup(B: int, N: int, M: int, K: int, device) -> int:
-    """The fused recursions' bands per workgroup at this shape on `device` (the library's
-    own choice, sdtw_fused_bands_per_workgroup): 2 or 4."""
+    """The fused forward recursions' bands per workgroup at this shape on `device` (the
+    library's own choice, sdtw_fused_bands_per_workgroup): 2 or 4."""
     with torch.cuda.device(device):
         return int(load().sdtw_fused_bands_per_workgroup(B, N, M, K))
 
