@@ -146,7 +146,9 @@ int sdtw_table_unpack_f32(const float *Rt, float *R, int64_t B, int64_t N, int64
 int sdtw_table_pack_f32(const float *R, float *Rt, int64_t B, int64_t N, int64_t M,
                         void *stream);
 
-/* Bytes of caller-provided scratch that `op` needs at this shape (0 if none). */
+/* Bytes of caller-provided scratch that `op` needs at this shape on the current device (0 if
+ * none): the fused recursions' workgroup geometry, and with it their scratch, follows the
+ * device's CU count.  A launch on a device that needs more reports SDTW_ERR_WORKSPACE. */
 size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K);
 
 /* D[b,i,j] = max(0, (|x_bi|^2 + |y_bj|^2) - 2 x_bi . y_bj)  -> D (B,N,M).

@@ -97,8 +97,13 @@ int fused_bwd_wmax(int64_t B, int64_t N, int64_t M, int64_t K) {
     if (mfma_costs(N, M, K) && B * dp_geom(N, 1).G <= cu_count()) return 1;
     return fused_wmax(B, N, M, K);
 }
-// workspace sizing: the 1-band geometry needs the most cross-workgroup rows
-int fused_ws_wmax(int64_t N, int64_t M, int64_t K) { return mfma_costs(N, M, K) ? 1 : 4; }
+// Workspace sizing: the geometry with the most cross-workgroup rows a launch can take.  The
+// forward's 2-band one whatever the device; the backward's 1-band one where it takes it on
+// this device (a launch on a device with fewer CUs then reports SDTW_ERR_WORKSPACE).
+int fused_ws_wmax(int64_t B, int64_t N, int64_t M, int64_t K, bool bwd) {
+    if (!mfma_costs(N, M, K)) return 4;
+    return bwd && fused_bwd_wmax(B, N, M, K) == 1 ? 1 : 2;
+}
 // Process-wide: whether the fused backward must give run-to-run identical bits
 // (sdtw_set_deterministic).
 std::atomic<int> g_deterministic{0};
@@ -320,11 +325,11 @@ size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) 
         case SDTW_OP_BWD:
             return ws_dp(B, N, M);
         case SDTW_OP_FUSED_FWD:
-            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(N, M, K));
+            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(B, N, M, K, false));
         case SDTW_OP_FUSED_BWD:
             if (fused_grad_mode(B, N, M, K))
-                return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(N, M, K));
-            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(N, M, K)) + align_up(sizeof(float) * B * N * M) +
+                return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(B, N, M, K, true));
+            return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(B, N, M, K, true)) + align_up(sizeof(float) * B * N * M) +
                    ws_dist_bwd(B, N, M, K);
         default:
             return 0;

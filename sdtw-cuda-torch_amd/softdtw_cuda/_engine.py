@@ -247,7 +247,10 @@ def _debug_check(op, ws, nws, B, N, M, K, what):
 
 
 def _workspace(op, B, N, M, K, device):
-    n = int(load().sdtw_workspace_bytes(op, B, N, M, K))
+    # the size can depend on the device (the fused recursions' workgroup geometry follows its
+    # CU count), so it is queried with that device current
+    with torch.cuda.device(device):
+        n = int(load().sdtw_workspace_bytes(op, B, N, M, K))
     if n == 0:
         return None, 0
     return torch.empty(n, dtype=torch.uint8, device=device), n
