@@ -19,7 +19,9 @@ pytestmark = pytest.mark.gpu
 
 # (B, N, M, K, gamma, bandwidth): every matrix-core width, ragged bands and tiles, a single
 # band, several workgroups per pair, 4-band workgroups (a batch whose 2-band workgroups do
-# not all fit on the GPU, K <= 16), a Sakoe-Chiba band, the headline shape
+# not all fit on the GPU, K <= 16), 2-band workgroups (a batch whose one-band workgroups do
+# not all fit: 80 pairs x 4 bands on a 256-CU GPU), a Sakoe-Chiba band, the headline shape
+# (one-band workgroups)
 CASES = [
     (3, 200, 150, 4, 1.0, -1.0),
     (2, 130, 300, 8, 0.5, -1.0),
@@ -29,6 +31,7 @@ CASES = [
     (2, 40, 70, 16, 1.0, -1.0),
     (1, 700, 180, 8, 0.3, -1.0),
     (160, 256, 64, 16, 1.0, -1.0),
+    (80, 256, 200, 64, 1.0, -1.0),
     (2, 300, 280, 16, 1.0, 40.0),
     (32, 512, 512, 64, 1.0, -1.0),
 ]
