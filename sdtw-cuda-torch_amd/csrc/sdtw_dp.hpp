@@ -1072,10 +1072,10 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // Where this lane's per-step store of the group at s0 goes (entry u for step u).  Lane
     // 63's ring stores are unconditional: slots of columns < 0 or >= M are never read before
     // being rewritten or at all.
+    // (the edge lane's address is wave-uniform, so one per-lane select picks it)
     auto step_dst = [&](int s0) -> double* {
-        if (l == WAVE - 1 && out_lds) return lout + hslot(s0 - (WAVE - 1));
-        if (l == WAVE - 1 && out_glb) return stage + (WAVE + U);
-        return stage + l;
+        double* edge = out_lds ? lout + hslot(s0 - (WAVE - 1)) : (out_glb ? stage + (WAVE + U) : stage + l);
+        return l == WAVE - 1 ? edge : stage + l;
     };
     // Hand the last row's columns computed by the group at s0 (lane 63 computed column
     // s0 + u - 63 at step s0 + u) to the band below: publish the ring entries lane 63 stored,
@@ -1397,9 +1397,10 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // where this lane's per-step stores of the group at q0 go (float4 entry u for step u,
     // x y z written); lane 0's ring stores are unconditional, as in the forward
     auto step_dst = [&](int q0) -> float* {
-        if (l == 0 && out_lds) return reinterpret_cast<float*>(lout + hslot(q0 - (WAVE - 1)));
-        if (l == 0 && out_glb) return reinterpret_cast<float*>(stage_glb);
-        return reinterpret_cast<float*>(stage + 12 * l);
+        float* own = reinterpret_cast<float*>(stage + 12 * l);
+        float* edge = out_lds ? reinterpret_cast<float*>(lout + hslot(q0 - (WAVE - 1)))
+                              : (out_glb ? reinterpret_cast<float*>(stage_glb) : own);
+        return l == 0 ? edge : own;
     };
     // hand the band's first row to the band above: lane 0 produced sequence numbers
     // q - 63 (= M - 1 - j) during the group at q0; publish the ring entries it stored (the
