@@ -294,9 +294,13 @@ def random_walks(Kseq, N, D, g):
 
 def run_configs(numerics):
     """BASELINE.json configs 0, 2, 3, 4 on the GPU (config 1 is the default run): fwd+bwd
-    ms per step with fresh leaf clones (plumbing: loss .mean(); the others .sum()), and the
-    barycenter's 100 iterations end to end."""
+    ms per step with fresh leaf clones (plumbing: loss .mean(); the others .sum()), the median
+    of three timed runs after a warm-up, and the barycenter's 100 iterations end to end."""
     import torch
+
+    def median_of_runs(step, steps, warmup, runs=3):
+        res = [time_steps(step, steps, warmup if r == 0 else 1) for r in range(runs)]
+        return statistics.median(r[0] for r in res), max(r[1] for r in res)
 
     from softdtw_cuda import SoftDTW, softdtw_barycenter
 
@@ -311,14 +315,14 @@ def run_configs(numerics):
         return step
 
     x, y = make_inputs(4, 64, 64, 8, seed=0)
-    ms, peak = time_steps(step_of(SoftDTW(gamma=1.0, fused=False), x.cuda(), y.cuda(), "mean"), 20, 3)
+    ms, peak = median_of_runs(step_of(SoftDTW(gamma=1.0, fused=False), x.cuda(), y.cuda(), "mean"), 20, 10)
     out["plumbing B=4 N=M=64 D=8 unfused"] = {"ms": round(ms, 4), "peak_mib": round(peak, 2)}
     log(f"[configs] plumbing: {ms:.3f} ms")
 
     x, y = make_inputs(16, 4096, 3072, 4, seed=0)
     X, Y = x.cuda(), y.cuda()
     for fused in (False, True):
-        ms, peak = time_steps(step_of(SoftDTW(gamma=0.1, fused=fused), X, Y, "sum"), 5, 1)
+        ms, peak = median_of_runs(step_of(SoftDTW(gamma=0.1, fused=fused), X, Y, "sum"), 5, 1)
         key = f"long B=16 N=4096 M=3072 D=4 gamma=0.1 {'fused' if fused else 'unfused'}"
         out[key] = {"ms": round(ms, 3), "peak_mib": round(peak, 1),
                     "cells_per_s": 16 * 4096 * 3072 / (ms * 1e-3)}
@@ -329,8 +333,8 @@ def run_configs(numerics):
     g = torch.Generator().manual_seed(0)
     x = sinusoids(64, 256, 16, g)
     y = sinusoids(64, 256, 16, g)
-    ms, peak = time_steps(step_of(SoftDTW(gamma=1.0, normalize=True, fused=True), x.cuda(),
-                                  y.cuda(), "sum"), 20, 3)
+    ms, peak = median_of_runs(step_of(SoftDTW(gamma=1.0, normalize=True, fused=True), x.cuda(),
+                                      y.cuda(), "sum"), 20, 10)
     out["normalize B=64 N=M=256 D=16 fused"] = {"ms": round(ms, 4), "peak_mib": round(peak, 2)}
     log(f"[configs] normalize: {ms:.3f} ms")
 

@@ -8,7 +8,7 @@ from torch import nn
 from . import _engine
 from ._device import compute_device
 from .autograd import SoftDTWAutograd, SoftDTWSqEuclidAutograd
-from .autograd_xy import SoftDTWXYAutograd
+from .autograd_xy import SoftDTWNormalizedXYAutograd, SoftDTWXYAutograd
 from .distances import pairwise_distance
 
 _SQEUCLID_NAMES = ("sqeuclidean", "sq_euclidean", "squared_euclidean")
@@ -100,13 +100,14 @@ class SoftDTW(nn.Module):
             x = x.to(dev)
             y = y.to(dev)
 
-        if self.normalize:
+        if self.normalize and use_fused:
+            # the concatenation trick below, as one autograd node (fewer host-side graph
+            # nodes and launches per step; the same values)
+            res = SoftDTWNormalizedXYAutograd.apply(x, y, self.gamma, self.bandwidth)
+        elif self.normalize:
             x_cat = torch.cat([x, x, y], dim=0)
             y_cat = torch.cat([y, x, y], dim=0)
-            if use_fused:
-                out = SoftDTWXYAutograd.apply(x_cat, y_cat, self.gamma, self.bandwidth)
-            else:
-                out = _unfused(x_cat, y_cat, self.gamma, self.bandwidth, self.dist)
+            out = _unfused(x_cat, y_cat, self.gamma, self.bandwidth, self.dist)
             out_xy, out_xx, out_yy = out.split(bx, dim=0)
             res = out_xy - 0.5 * (out_xx + out_yy)
         elif use_fused:

@@ -255,6 +255,30 @@ def test_unfused_normalize_matches_two_node_graph():
     torch.testing.assert_close(ya.grad, yb.grad, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_fused_normalize_node_matches_concatenation_graph(dtype):
+    # normalize=True, fused=True runs one autograd node (SoftDTWNormalizedXYAutograd); the
+    # reference's concatenation trick as separate graph nodes gives the same loss bits and the
+    # same gradients up to the order the three appearances of each input are summed in
+    from softdtw_cuda import SoftDTW
+    from softdtw_cuda.autograd_xy import SoftDTWXYAutograd
+
+    x, y = randn_pair(4, 96, 96, 16, seed=12)
+    x, y = x.to(dtype), y.to(dtype)
+    xa, ya = x.cuda().requires_grad_(True), y.cuda().requires_grad_(True)
+    out_a = SoftDTW(gamma=0.7, normalize=True, fused=True)(xa, ya)
+    (out_a * torch.arange(1, 5, device="cuda", dtype=dtype)).sum().backward()
+    xb, yb = x.cuda().requires_grad_(True), y.cuda().requires_grad_(True)
+    out = SoftDTWXYAutograd.apply(torch.cat([xb, xb, yb]), torch.cat([yb, xb, yb]), 0.7, None)
+    o_xy, o_xx, o_yy = out.split(4, dim=0)
+    out_b = o_xy - 0.5 * (o_xx + o_yy)
+    (out_b * torch.arange(1, 5, device="cuda", dtype=dtype)).sum().backward()
+    assert torch.equal(out_a, out_b)
+    tol = dict(rtol=1e-6, atol=1e-6) if dtype == torch.float32 else dict(rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(xa.grad, xb.grad, **tol)
+    torch.testing.assert_close(ya.grad, yb.grad, **tol)
+
+
 def _same_R(Rc, Ro):
     """R tables equal as the CPU path leaves them: NaN where it has NaN, the same infinities,
     and every finite value with the same bits."""
