@@ -128,12 +128,16 @@ size_t sdtw_dist_record_bytes(int64_t B, int64_t N, int64_t M);
 int sdtw_set_deterministic(int on);
 
 /* Bands per workgroup the fused forward recursions (sdtw_fused_fwd_f32, sdtw_fused_fwd_d_f32)
- * take at this shape on the current device: 2 when the batch's 2-band workgroups all fit on
- * the GPU at once (their matrix-core producer waves then have SIMDs of their own), else 4; 0
- * for an invalid shape.  The choice the launcher makes, exported so a caller can choose
- * between sdtw_fused_fwd_d_f32 and the two-call unfused forward.  (The fused backward,
- * sdtw_fused_bwd_f32 and sdtw_fused_bwd_e_f32, takes 1 where the batch's one-band workgroups
- * all fit, else the same.)  No counterpart in the reference. */
+ * take for an unbanded call at this shape on the current device under the current
+ * arithmetic: 1 when the batch's one-band workgroups all fit on the GPU at once and the
+ * arithmetic is exact or mixed (the scaled linear-domain recursion, whose compute, producer,
+ * helper and converter waves then have a SIMD each), else 2 when the 2-band workgroups all
+ * fit (their matrix-core producer waves have SIMDs of their own), else 4; 0 for an invalid
+ * shape.  (A banded call takes 2 where this is 1.)  The choice the launcher makes, exported
+ * so a caller can choose between sdtw_fused_fwd_d_f32 and the two-call unfused forward.
+ * (The fused backward, sdtw_fused_bwd_f32 and sdtw_fused_bwd_e_f32, takes 1 where the
+ * batch's one-band workgroups all fit, else 2 or 4 as here.)  No counterpart in the
+ * reference. */
 int sdtw_fused_bands_per_workgroup(int64_t B, int64_t N, int64_t M, int64_t K);
 
 /* Number of floats of the R table for B pairs of N x M cells. */

@@ -97,12 +97,13 @@ int fused_bwd_wmax(int64_t B, int64_t N, int64_t M, int64_t K) {
     if (mfma_costs(N, M, K) && B * dp_geom(N, 1).G <= cu_count()) return 1;
     return fused_wmax(B, N, M, K);
 }
-// Workspace sizing: the geometry with the most cross-workgroup rows a launch can take.  The
-// forward's 2-band one whatever the device; the backward's 1-band one where it takes it on
-// this device (a launch on a device with fewer CUs then reports SDTW_ERR_WORKSPACE).
+// Workspace sizing: the geometry with the most cross-workgroup rows a launch can take: the
+// 1-band one where either direction takes it on this device (a launch on a device with fewer
+// CUs then reports SDTW_ERR_WORKSPACE), else the 2-band one.
 int fused_ws_wmax(int64_t B, int64_t N, int64_t M, int64_t K, bool bwd) {
+    (void)bwd;
     if (!mfma_costs(N, M, K)) return 4;
-    return bwd && fused_bwd_wmax(B, N, M, K) == 1 ? 1 : 2;
+    return fused_bwd_wmax(B, N, M, K) == 1 ? 1 : 2;
 }
 // Process-wide: whether the fused backward must give run-to-run identical bits
 // (sdtw_set_deterministic).
@@ -210,6 +211,15 @@ std::atomic<int> g_numerics{SDTW_NUMERICS_MIXED};
 bool exact_forward() { return g_numerics.load(std::memory_order_relaxed) != SDTW_NUMERICS_FAST; }
 bool exact_backward() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_EXACT; }
 
+// The fused forward: one band per workgroup where the batch's one-band workgroups all fit
+// and the call takes the scaled linear-domain recursion (exact arithmetic, matrix-core
+// costs, no band): its compute, producer, helper and converter waves then have a SIMD each.
+// Otherwise fused_wmax.
+int fused_fwd_wmax(int64_t B, int64_t N, int64_t M, int64_t K, double bandwidth) {
+    if (exact_forward() && !(bandwidth > 0.0) && fused_bwd_wmax(B, N, M, K) == 1) return 1;
+    return fused_wmax(B, N, M, K);
+}
+
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mu;
@@ -268,7 +278,7 @@ size_t sdtw_dist_record_bytes(int64_t B, int64_t N, int64_t M) {
 
 int sdtw_fused_bands_per_workgroup(int64_t B, int64_t N, int64_t M, int64_t K) {
     if (!shape_ok(B, N, M, K, true)) return 0;
-    return fused_wmax(B, N, M, K);
+    return fused_fwd_wmax(B, N, M, K, -1.0);
 }
 
 int sdtw_debug_status(int op, const void* ws, size_t ws_bytes, int64_t B, int64_t N, int64_t M,
@@ -464,7 +474,7 @@ static int fused_fwd_common(const float* x, const float* y, float* D, void* reco
     Carver c{static_cast<char*>(ws), ws_bytes};
     float* x2 = c.take<float>(B * N);
     float* y2 = c.take<float>(B * M);
-    const int wmax = fused_wmax(B, N, M, K);
+    const int wmax = fused_fwd_wmax(B, N, M, K, bandwidth);
     const DPScratch d = carve_dp(c, B, N, M, wmax);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     DPParams p{};
@@ -478,6 +488,9 @@ static int fused_fwd_common(const float* x, const float* y, float* D, void* reco
     p.R = R;
     p.out = out;
     p.D_out = D;
+    // pairs whose norms allow it take the scaled linear-domain recursion (exact arithmetic,
+    // matrix-core costs, no band, up to 2 bands per workgroup)
+    p.lin = exact_forward() && !(p.bw > 0.0) && mfma_costs(N, M, K) && p.W <= 2 ? 1 : 0;
     if (D && record) {  // the distance record: clamp flags, and the norms formed here
         const DistRecord rec = dist_record(record, B, N, M);
         p.clamped = rec.clamped;

@@ -14,7 +14,7 @@ __global__ void prep_kernel(int* ticket, int* err, unsigned long long* rows, int
 
 hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st) {
     const int64_t entries = (int64_t)P.B * P.G * P.RW;
-    const int64_t nwords = bwd ? 2 * entries : entries;
+    const int64_t nwords = bwd || P.lin ? 2 * entries : entries;  // 16-byte entries
     const unsigned long long lo = bwd ? (unsigned long long)kEmpty32 : kEmpty64;
     const unsigned long long hi = bwd ? 0ull : kEmpty64;
     if (P.x2_fill) {  // with the fused recursions' row norms (and the gradient mode's zeroing)

@@ -377,8 +377,8 @@ struct CostMfma {
     int M, K;
     float xa[4][NKK];  // A: x[row0 + 16 rb + (l & 15)][4 kk + (l >> 4)]
     float x2o[4][4];   // norms of the output rows row0 + 16 rb + 4 (l >> 4) + r
-    float yb[NKK];     // B: y[c0 + (l & 15)][4 kk + (l >> 4)]
-    float y2n, y2c;    // norm of the issued / the begun tile's column
+    float yb[2][NKK];  // B: y[c0 + (l & 15)][4 kk + (l >> 4)], two tiles in flight
+    float y2n[2], y2c; // norm of the issued / the begun tile's column
     bool tile_bad;     // the last finished tile holds a non-finite cost (wave-uniform)
     bool tile_nonpos;  // ... a cost that is not positive (0 or NaN; wave-uniform)
     floatx4 acc[4];
@@ -403,24 +403,33 @@ struct CostMfma {
             for (int r = 0; r < 4; ++r) x2o[rb][r] = x2[min(row0 + 16 * rb + 4 * (l >> 4) + r, N - 1)];
         }
     }
+    // operands of the tile at column c0 into slot S (a producer wave keeps two tiles of
+    // loads in flight, so a tile's y rows arrive while the tile before it is multiplied)
+    // (FULL: K == KX, every load inside the row, issued unconditionally: a fixed count of
+    // memory operations per tile; else only the loads inside K)
+    template <int S = 0, bool FULL = false>
     SDTW_DEV void issue(int c0) {
         const int l = threadIdx.x & (WAVE - 1);
         const int col = min(max(c0 + (l & 15), 0), M - 1);
+        const float* yc = y + (int64_t)col * K;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
             const int k = 4 * kk + (l >> 4);
-            yb[kk] = (k < K) ? y[(int64_t)col * K + k] : 0.0f;
+            if constexpr (FULL) yb[S][kk] = yc[k];
+            else yb[S][kk] = (k < K) ? yc[k] : 0.0f;
         }
-        y2n = y2[col];
+        y2n[S] = y2[col];
     }
     // k-step kk of the tile's products (four independent accumulation chains)
+    template <int S = 0>
     SDTW_DEV void mma(int kk) {
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
-            acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[rb][kk], yb[kk], acc[rb], 0, 0, 0);
+            acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[rb][kk], yb[S][kk], acc[rb], 0, 0, 0);
     }
+    template <int S = 0>
     SDTW_DEV void zero() {
-        y2c = y2n;
+        y2c = y2n[S];
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) acc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -473,20 +482,42 @@ struct CostMfma {
         tile_nonpos = __builtin_amdgcn_ballot_w64(!(mn > 0.0f)) != 0;
     }
     // the same tile into the pair's cost tensor Dp (N, M): lane l's column c0 + (l & 15) of
-    // rows row0 + 16 rb + 4 (l >> 4) + r, 16 lanes per 64-byte row segment
+    // rows row0 + 16 rb + 4 (l >> 4) + r, 16 lanes per 64-byte row segment.  UNIF: entries of
+    // rows >= N or columns >= M were formed from the last row's / column's operands (clamped
+    // indices), so they are stored to that row / column, which then receives its own bits
+    // again: every lane stores every entry, with no branch (a fixed count of memory
+    // operations per tile); else those entries are skipped.
+    template <bool UNIF = false>
     SDTW_DEV void store_d(float* Dp, int c0, int row0, int N) const {
         const int l = threadIdx.x & (WAVE - 1);
-        const int col = c0 + (l & 15);
-        if ((unsigned)col >= (unsigned)M) return;
+        if constexpr (UNIF) {
+            const int col = min(max(c0 + (l & 15), 0), M - 1);
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+            for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = row0 + 16 * rb + 4 * (l >> 4) + r;
-                if (row < N) Dp[(int64_t)row * M + col] = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const int row = min(row0 + 16 * rb + 4 * (l >> 4) + r, N - 1);
+                    Dp[(int64_t)row * M + col] = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
+                }
+        } else {
+            const int col = c0 + (l & 15);
+            if ((unsigned)col >= (unsigned)M) return;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = row0 + 16 * rb + 4 * (l >> 4) + r;
+                    if (row < N) Dp[(int64_t)row * M + col] = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
+                }
+        }
     }
 };
+
+// the matrix-core width of a cost source (0: not matrix-core tiles)
+template <class C>
+struct KXOf : std::integral_constant<int, 0> {};
+template <int KX>
+struct KXOf<CostMfma<KX>> : std::integral_constant<int, KX> {};
 
 // Fused fallback (features beyond the register-resident width, and the tiny problems whose
 // reference dot is ATen's multiply-then-add kernel): each lane computes its 16 tile entries
@@ -621,6 +652,11 @@ struct Smem {
     // backward, gradient mode: G tiles copied out of the band's cost ring by its gradient
     // waves, for dL/dx (ints 48 .. 51) and for dL/dy (ints 52 .. 55)
     SDTW_DEV int* gdone() const { return reinterpret_cast<int*>(base) + 48; }
+    // forward, linear domain: groups staged by band w's compute wave (ints 56, 57) and
+    // converted by its converter wave (58, 59); the pair's norm maxima and bad flag (60 .. 62)
+    SDTW_DEV int* lin_staged() const { return reinterpret_cast<int*>(base) + 56; }
+    SDTW_DEV int* lin_done() const { return reinterpret_cast<int*>(base) + 58; }
+    SDTW_DEV unsigned* lin_red() const { return reinterpret_cast<unsigned*>(base) + 60; }
     SDTW_DEV double* tables() const { return tab; }
     SDTW_DEV unsigned char* ring() const { return base + 256; }
     SDTW_DEV float* cost_ring(int w) const {
@@ -697,7 +733,7 @@ struct GTile {
 // Gradient mode (GRAD, backward only): the band's gradient waves copy each G tile out of the
 // slots instead, counting the tiles in gdone (one count per gradient part); the producer
 // then waits for both counts >= t - 3 (which implies done >= t - 3) and stores no G tile.
-template <class Src, bool BWD, bool GRAD = false>
+template <class Src, bool BWD, bool GRAD = false, bool DST = false, bool DB = false>
 SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int w) {
     constexpr bool MMA = !std::is_same<Src, CostD>::value;
     static_assert(!GRAD || (BWD && MMA), "gradient mode: fused backward only");
@@ -714,18 +750,38 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
     const int groups = P.S / U;  // groups of the compute wave
     const int T = groups + 1;    // tiles it reads
     auto col = [&](int t) { return BWD ? P.M - TC * (t + 1) : TC * t; };
-    c.issue(col(0));
-    for (int t = 0; t < T; ++t) {
+    // matrix-core tiles: the operands of the next tile are loaded once this one has been
+    // multiplied.  With DB (K == KX, and a kernel whose register budget holds it) there are
+    // two operand slots and the loads of tile t + 2 go to slot t & 1, so each has a whole
+    // tile's time to arrive; every tile then issues the same memory operations (the loads
+    // at clamped columns past the table, and the stores of D in full, DST: P.D_out set), so
+    // the wait before a tile's products covers only the loads it needs.
+    static_assert(!DST || (MMA && !BWD), "D stores: forward matrix-core tiles only");
+    static_assert(!DB || MMA, "two operand slots: matrix-core tiles only");
+    if constexpr (DB) {
+        // (scheduling barriers keep each slot's loads together and in slot order, which the
+        // waits count on)
+        c.template issue<0, true>(col(0));
+        __builtin_amdgcn_sched_barrier(0);
+        c.template issue<1, true>(col(1));
+        __builtin_amdgcn_sched_barrier(0);
+    } else if constexpr (MMA) {
+        c.template issue<0>(col(0));
+    } else {
+        c.issue(col(0));
+    }
+    auto tile = [&](int t, auto slot_tag) -> bool {
+        constexpr int SL = DB ? decltype(slot_tag)::value : 0;
         if constexpr (MMA) {
-            c.zero();
+            c.template zero<SL>();
 #pragma unroll
-            for (int kk = 0; kk < Src::NKK; ++kk) c.mma(kk);
+            for (int kk = 0; kk < Src::NKK; ++kk) c.template mma<SL>(kk);
         }
         const int need = BWD ? t - 3 : t - 4;
         if (need > 0 && (!wait_at_least(done, need, known, P.err, P.spin_limit) ||
                          (GRAD && !wait_at_least(done_y, need, known_y, P.err, P.spin_limit)))) {
             give_up<BWD>(P, p, b);
-            return;
+            return false;
         }
         GTile gt;
         const bool flush = BWD && !GRAD && t >= 4;
@@ -740,12 +796,21 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
             }
         }
         if ((threadIdx.x & (WAVE - 1)) == 0) lds_publish(ready, t + 1);
-        if (t + 1 < T) c.issue(col(t + 1));
+        if constexpr (DB) {
+            __builtin_amdgcn_sched_barrier(0);
+            c.template issue<SL, true>(col(t + 2));
+            __builtin_amdgcn_sched_barrier(0);
+        } else if constexpr (MMA) {
+            if (t + 1 < T) c.template issue<0>(col(t + 1));
+        } else {
+            if (t + 1 < T) c.issue(col(t + 1));
+        }
         // unfused mode's cost tensor, from the same tile (forward; after the next loads, so
         // that they do not queue behind these stores), and the pair's clamp record
+        // (DST: the stores are compiled in; without DB they follow P.D_out at run time)
         if constexpr (MMA && !BWD) {
-            if (P.D_out) {
-                c.store_d(P.D_out + (int64_t)p * P.N * P.M, col(t), b * WAVE, P.N);
+            if (DST || (!DB && P.D_out)) {
+                c.template store_d<DB>(P.D_out + (int64_t)p * P.N * P.M, col(t), b * WAVE, P.N);
                 if (P.clamped && c.tile_nonpos && !clamp_marked) {
                     clamp_marked = true;
                     if ((threadIdx.x & (WAVE - 1)) == 0) P.clamped[p] = 1;
@@ -753,6 +818,18 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
             }
         }
         if (flush) gt.write(P, p, b);
+        return true;
+    };
+    using S0_ = std::integral_constant<int, 0>;
+    using S1_ = std::integral_constant<int, 1>;
+    if constexpr (DB) {
+        for (int t = 0; t < T; t += 2) {
+            if (!tile(t, S0_{})) return;
+            if (t + 1 < T && !tile(t + 1, S1_{})) return;
+        }
+    } else {
+        for (int t = 0; t < T; ++t)
+            if (!tile(t, S0_{})) return;
     }
     if (BWD && !GRAD) {
         for (int g = max(T - 4, 0); g < groups; ++g) {
@@ -986,6 +1063,33 @@ SDTW_HD size_t ring_bytes_fwd(int W) { return ((size_t)(W + 1) * RS + kStageFwd)
 constexpr int kStageBwd = 12 * WAVE + 16 * U + 16 * U;
 SDTW_HD size_t ring_bytes_bwd(int W) { return (size_t)(W + 1) * RS * sizeof(float4) + kStageBwd; }
 
+// Forward in the scaled linear domain (fwd_band_lin): LDS after the staging block.  The
+// handoff rings keep their p values in the slots of the log-domain rings; their exponents
+// follow the staging block as W + 1 rings of RS ints; then each band's converter stage: two
+// buffers (groups alternate) of 64 lane rows of kLinRow entries (p as doubles, then e as
+// ints; the row pitch of 17 keeps a wave's accesses to one column conflict-free).
+constexpr int kLinNeg = -(1 << 30);  // exponent of a zero value (R = +inf)
+constexpr int kLinRow = U + 1;
+constexpr int kLinBuf = WAVE * kLinRow;
+SDTW_HD size_t lin_extra_bytes(int W) { return (size_t)(W + 1) * RS * 4 + (size_t)W * 2 * kLinBuf * 12; }
+SDTW_DEV int* lin_ering(const Smem& sm) { return reinterpret_cast<int*>(sm.ring() + ring_bytes_fwd(sm.W)); }
+SDTW_DEV double* lin_stage_p(const Smem& sm, int w, int k) {
+    return reinterpret_cast<double*>(lin_ering(sm) + (sm.W + 1) * RS) + (w * 2 + k) * kLinBuf;
+}
+SDTW_DEV int* lin_stage_e(const Smem& sm, int w, int k) {
+    return reinterpret_cast<int*>(lin_stage_p(sm, sm.W, 0)) + (w * 2 + k) * kLinBuf;
+}
+// Cross-workgroup rows of the forward: 8-byte entries (R), or in a launch that can take the
+// linear domain 16-byte ones, (p, then e and the tag 1), written and read as two 64-bit
+// halves, each whole or empty.  All rows of such a launch are 16-byte pitched, so the rows
+// of its log-domain pairs (8-byte entries, first half) and linear-domain pairs do not overlap.
+SDTW_HD int64_t fwd_row_pitch(const DPParams& P) { return P.lin ? 2 * (int64_t)P.RW : P.RW; }
+SDTW_DEV void glb_put_lin(double2* q, double pv, int ev) {
+    unsigned long long* a = reinterpret_cast<unsigned long long*>(q);
+    __hip_atomic_store(a, (unsigned long long)__double_as_longlong(pv), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a + 1, (1ull << 32) | (unsigned)ev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------------------
@@ -1011,7 +1115,7 @@ SDTW_DEV void fwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     const bool out_lds = (b + 1 < nb) && (w + 1 < W);
     const bool out_glb = (b + 1 < nb) && (w + 1 == W);
     // cross-workgroup row of this workgroup: RW = M + 2*RPAD entries, column c at RPAD + c
-    double* gout = P.gring + ((int64_t)p * G + g) * P.RW + RPAD;
+    double* gout = P.gring + ((int64_t)p * G + g) * fwd_row_pitch(P) + RPAD;
     const double* lin = lring + w * RS;
     double* lout = lring + (w + 1) * RS;
     const int* lin_flag = sm.prod() + w;
@@ -1264,14 +1368,381 @@ SDTW_DEV void helper_wave(const DPParams& P, const Smem& sm, const T* gin, int k
 // With W = 2, matrix-core producers take the SIMDs the compute waves leave free under
 // round-robin wave placement; with W = 4 (large batches, see the launcher) every producer
 // shares its compute wave's SIMD, as D producers (backward) always do.
+// ---------------------------------------------------------------------------------------
+// Forward in the scaled linear domain.
+//
+// The recursion R = d + softmin(R_diag, R_up, R_left) (launcher.py:317-322) is the log of a
+// linear one: with P = exp(-R / gamma),  P(i,j) = exp(-d(i,j) / gamma) (P_diag + P_up +
+// P_left).  Each P is held as p 2^e (p a double, e an int), so nothing underflows: a step
+// aligns the three predecessors to their largest exponent (ldexp, exact), adds them and
+// multiplies by the cost's exponential pD 2^eD.  No exp or log is on the dependency chain:
+// pD depends on the cost alone, and a converter wave per band turns p 2^e back into
+// R = -gamma log(p 2^e) for the R table, on a SIMD of its own.  p is renormalised (frexp)
+// once per group and stays within [0.48, 2^42) in between; a zero (R = +inf: the padding,
+// inactive lanes) is (0, kLinNeg), which no maximum of exponents picks over a live value.
+// Rounding: P carries a relative error of a few units in the last place per cell, that is R
+// an absolute one of a few gamma 2^-53, below the ulp(R) per cell of the log-domain form;
+// R is rounded once to fp32 by the converter.  A pair takes this path when its row norms
+// are finite and bound every cost so that no exponent nears 2^29 (lin_pair_ok); the others
+// run fwd_band in the same launch.
+// ---------------------------------------------------------------------------------------
+
+// exp(-d / gamma) = pD 2^eD, pD in [0.998, 2.003): exp_tab_abs's reduction with the power
+// of two kept apart (T is the folded table: entry j << 12 is put back into its high word).
+SDTW_DEV void lin_cost(float d, double ninv_gamma, const double* T, double& pD, int& eD) {
+    const double xc = (double)d * ninv_gamma;
+    const double tc = fm::exp_tab_abs_tc(xc);
+    const int k = fm::lo_word(tc);
+    const int j = k & (fm::kExpTabN - 1);
+    const double tf = T[j];
+    const double em1 = fm::exp_tab_abs_em1(xc, tc);
+    const double t = fm::from_words(fm::hi_word(tf) + (j << 12), fm::lo_word(tf));
+    pD = ::fma(t, em1, t);
+    eD = k >> 8;  // floor(k / 256)
+}
+
+// R = -gamma log(p 2^e): p = m 2^k with m in [1, 2), log m by log_tab_1to3, (e + k - 1) ln2
+// in two parts (each fma forms its product exactly), then one rounding for the product with
+// -gamma.  p = 0 gives +inf.
+SDTW_DEV double lin_to_R(double pv, int ev, double ngamma, const double* L) {
+    const int k = __builtin_amdgcn_frexp_exp(pv);
+    const double m = 2.0 * __builtin_amdgcn_frexp_mant(pv);
+    const double ef = (double)(ev + k - 1);
+    const double t = ::fma(ef, fm::kLn2Hi, ::fma(ef, fm::kLn2Lo, fm::log_tab_1to3(m, L)));
+    return pv == 0.0 ? dinf() : ngamma * t;
+}
+
+// Whether pair p takes the linear domain: every row norm finite, and the cost bound
+// d <= 2 (|x_i|^2 + |y_j|^2) (2.01 for the fp32 evaluation) keeps each cost's k = 256 n + j
+// below 2^30 and every exponent along a path of N + M + 1 cells below 2^29 in magnitude.
+// Called by every thread of the workgroup (it holds a barrier); the workgroups of a pair
+// read the same norms and take the same decision.
+SDTW_DEV bool lin_pair_ok(const DPParams& P, const Smem& sm, int p) {
+    unsigned* red = sm.lin_red();  // zeroed before the kernel's first barrier
+    float mx = 0.0f, my = 0.0f;
+    bool bad = false;
+    for (int e = threadIdx.x; e < P.N; e += blockDim.x) {
+        const float v = P.x2[(int64_t)p * P.N + e];
+        bad = bad || !(v <= 1e30f);
+        mx = fmaxf(mx, v);
+    }
+    for (int e = threadIdx.x; e < P.M; e += blockDim.x) {
+        const float v = P.y2[(int64_t)p * P.M + e];
+        bad = bad || !(v <= 1e30f);
+        my = fmaxf(my, v);
+    }
+    if (bad) atomicOr(red + 2, 1u);
+    atomicMax(red, __float_as_uint(mx));  // non-negative floats order as their bits
+    atomicMax(red + 1, __float_as_uint(my));
+    __syncthreads();
+    if (red[2] != 0u) return false;
+    const double xmax = 2.01 * ((double)__uint_as_float(red[0]) + (double)__uint_as_float(red[1])) * P.inv_gamma;
+    return xmax * fm::kInvLn2x256 < 1073741824.0 &&
+           (double)(P.N + P.M + 2) * (xmax * 1.4426950408889634 + 4.0) < 536870912.0;
+}
+
+template <class Cost>
+SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p, int g, int w) {
+    const int l = threadIdx.x & (WAVE - 1);
+    const int W = P.W, G = P.G, nb = P.nb, N = P.N, M = P.M, S = P.S;
+    const int b = g * W + w;
+    const bool row_ok = b * WAVE + l < N;
+    const double ninv_gamma = -P.inv_gamma;
+    const double* tabE = sm.tables();
+    float* cring = sm.cost_ring(w);
+    const float* crow = cring + l * CS;
+    const bool out_lds = (b + 1 < nb) && (w + 1 < W);
+    const bool out_glb = (b + 1 < nb) && (w + 1 == W);
+    double* pring = reinterpret_cast<double*>(sm.ring());
+    int* ering = lin_ering(sm);
+    const double* in_p = pring + w * RS;
+    const int* in_e = ering + w * RS;
+    double* out_p = pring + (w + 1) * RS;
+    int* out_e = ering + (w + 1) * RS;
+    double2* gout = reinterpret_cast<double2*>(P.gring) + ((int64_t)p * G + g) * P.RW + RPAD;
+    const int* in_flag = sm.prod() + w;
+    int* staged = sm.lin_staged() + w;
+    const int* conv = sm.lin_done() + w;
+
+    int known_in = 0, known_free = 0, known_conv = 0;
+    double lp = 0.0;  // this lane's value one step ago (its left; lane l+1's up by DPP)
+    int le = kLinNeg;
+    double dp = (b == 0 && l == 0) ? 1.0 : 0.0;  // diagonal: R[0,0] = 0 above-left of cell (0, 0)
+    int de = (b == 0 && l == 0) ? 0 : kLinNeg;
+    double up_p[U];
+    int up_e[U];
+    float d_cur[U], d_nxt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {  // band 0: the +inf row above the table
+        up_p[u] = 0.0;
+        up_e[u] = kLinNeg;
+    }
+
+    // Band above: entries c0 .. c0 + U - 1 of its last row (lane 0's up values) from the LDS
+    // ring, as fwd_band's fetch_lds.  Past column M - 1 lane 0 is inactive.
+    auto fetch = [&](int c0) -> bool {
+        if (b == 0) return true;
+        const bool live = c0 < M;
+        const int need = min(c0 + U, M);
+        known_in = max(known_in, __builtin_amdgcn_readfirstlane(lds_load(in_flag)));
+        if (live && known_in < need && !wait_at_least(in_flag, need, known_in, P.err, P.spin_limit))
+            return false;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the ring reads stay after the count
+        const double* blk = in_p + hslot(c0 + 1);  // entries c0 + 1 .. c0 + U - 1
+        up_p[0] = in_p[hslot(c0)];
+        const double2* src = reinterpret_cast<const double2*>(blk);
+#pragma unroll
+        for (int k = 0; k < U / 2 - 1; ++k) {
+            const double2 v = src[k];
+            up_p[1 + 2 * k] = v.x;
+            up_p[2 + 2 * k] = v.y;
+        }
+        up_p[U - 1] = blk[U - 2];
+        const int* eblk = in_e + hslot(c0 + 1);  // a multiple of 16 slots: 16-byte aligned
+        up_e[0] = in_e[hslot(c0)];
+        const int4* esrc = reinterpret_cast<const int4*>(eblk);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int4 v = esrc[k];
+            up_e[1 + 4 * k] = v.x;
+            up_e[2 + 4 * k] = v.y;
+            up_e[3 + 4 * k] = v.z;
+            up_e[4 + 4 * k] = v.w;
+        }
+        up_e[13] = eblk[12];
+        up_e[14] = eblk[13];
+        up_e[15] = eblk[14];
+        if (live && l == 0) lds_publish(sm.cons() + w, need);
+        return true;
+    };
+
+    // One group of U steps from s0 (pipeline as fwd_band's).  Each step's values go to the
+    // lane's row of the converter stage (buffer (s0 / U) & 1), except lane 63's when a band
+    // of this workgroup is below: those go to the handoff ring, where the converter reads
+    // them too.  INTERIOR: every lane inside the table for all U steps (no masking).
+    auto group = [&](int s0, auto interior_tag) -> int {
+        constexpr bool INTERIOR = decltype(interior_tag)::value;
+#pragma unroll
+        for (int u = 0; u < U; ++u) d_cur[u] = d_nxt[u];
+        if (!cost.begin(cring, s0 + 2 * TC) || !fetch(s0)) return -1;
+        if (out_lds) {
+            const int need_free = s0 + U - WAVE + 1 - RS;
+            if (need_free > 0 && !wait_at_least(sm.cons() + (w + 1), need_free, known_free, P.err, P.spin_limit))
+                return -1;
+        }
+        // the stage buffer of this group was last read by the converter for group gi - 2
+        const int gi = s0 / U;
+        if (gi >= 2 && !wait_at_least(conv, gi - 1, known_conv, P.err, P.spin_limit)) return -1;
+        const int k = gi & 1;
+        const bool edge = out_lds && l == WAVE - 1;
+        double* sp = edge ? out_p + hslot(s0 - (WAVE - 1)) : lin_stage_p(sm, w, k) + l * kLinRow;
+        int* se = edge ? out_e + hslot(s0 - (WAVE - 1)) : lin_stage_e(sm, w, k) + l * kLinRow;
+        const float* dn = crow + ((s0 + TC - l) & (CR - 1));  // next group's costs
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            double pD;
+            int eD;
+            lin_cost(d_cur[u], ninv_gamma, tabE, pD, eD);
+            const double upp = shr1(up_p[u], lp);
+            const int upe = dpp_shr1(up_e[u], le);
+            const int em = max(max(upe, le), de);
+            const double sum = (::ldexp(upp, upe - em) + ::ldexp(lp, le - em)) + ::ldexp(dp, de - em);
+            double q = sum * pD;
+            int en = em + eD;
+            if (u == U - 1) {
+                en += __builtin_amdgcn_frexp_exp(q);
+                q = __builtin_amdgcn_frexp_mant(q);
+            }
+            if constexpr (!INTERIOR) {
+                const int j = s0 + u - l;
+                const bool act = row_ok && (unsigned)j < (unsigned)M;
+                q = act ? q : 0.0;
+                en = act ? en : kLinNeg;
+            }
+            dp = upp;
+            de = upe;
+            lp = q;
+            le = en;
+            sp[u] = q;
+            se[u] = en;
+            d_nxt[u] = dn[u];
+            cost.step(u, s0 + 2 * TC, s0 + 3 * TC);
+        }
+        cost.end(cring, s0 + 2 * TC, s0 + 3 * TC);
+        if (l == 0) lds_publish(staged, gi + 1);
+        if (out_lds) {
+            if (l == WAVE - 1) lds_publish(sm.prod() + (w + 1), min(max(s0 + U - (WAVE - 1), 0), M));
+        } else if (out_glb && l >= WAVE - U) {
+            // lane 63's values of this group (columns s0 - 63 .. s0 - 48, inside the row's
+            // padding) from its stage row to the cross-workgroup row
+            const int u = l - (WAVE - U);
+            const double pv = lin_stage_p(sm, w, k)[(WAVE - 1) * kLinRow + u];
+            const int ev = lin_stage_e(sm, w, k)[(WAVE - 1) * kLinRow + u];
+            glb_put_lin(gout + (s0 - (WAVE - 1)) + u, pv, ev);
+        }
+        return 0;
+    };
+
+    if (!cost.prologue(cring, 0) || !cost.prologue(cring, TC)) return give_up_fwd(P, p);
+    cost.preload(2 * TC);
+    {
+        const float* dn = crow + ((-l) & (CR - 1));
+#pragma unroll
+        for (int u = 0; u < U; ++u) d_nxt[u] = dn[u];
+    }
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool full = (b + 1) * WAVE <= N;
+    const int q_in = full ? min(WAVE, S) : S;
+    const int q_out = full ? max((M - U) / U * U + U, WAVE) : S;
+    int s0 = 0;
+    for (; s0 < q_in; s0 += U)
+        if (group(s0, F_{}) != 0) return give_up_fwd(P, p);
+    for (; s0 < min(q_out, S); s0 += U)
+        if (group(s0, T_{}) != 0) return give_up_fwd(P, p);
+    for (; s0 < S; s0 += U)
+        if (group(s0, F_{}) != 0) return give_up_fwd(P, p);
+}
+
+// The helper wave of a linear-domain pair: helper_wave for 16-byte (p, e) entries.
+SDTW_DEV void helper_wave_lin(const DPParams& P, const Smem& sm, const double2* gin) {
+    const int l = threadIdx.x & (WAVE - 1);
+    const int M = P.M;
+    double* ring_p = reinterpret_cast<double*>(sm.ring());
+    int* ring_e = lin_ering(sm);
+    int known_free = 0;
+    unsigned spins = 0;
+    for (int c = 0; c < M;) {
+        const int need_free = c + WAVE - RS;
+        if (need_free > 0 && !wait_at_least(sm.cons(), need_free, known_free, P.err, P.spin_limit)) return;
+        const int e = c + l;
+        double pv = 0.0;
+        int ev = 0;
+        bool empty = false;
+        if (e < M) {
+            const unsigned long long* a = reinterpret_cast<const unsigned long long*>(gin + e);
+            const unsigned long long lo = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned long long hi = __hip_atomic_load(a + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            pv = __longlong_as_double((long long)lo);
+            ev = (int)(unsigned)hi;
+            empty = lo == kEmpty64 || (unsigned)(hi >> 32) != 1u;
+        }
+        const unsigned long long miss = __ballot(empty);
+        const int n = miss ? (int)__builtin_ctzll(miss) : WAVE;  // leading written entries
+        if (l < n && e < M) {
+            ring_p[hslot(e)] = pv;
+            ring_e[hslot(e)] = ev;
+        }
+        if (n > 0) {
+            c = min(c + n, M);
+            if (l == 0) lds_publish(sm.prod(), c);
+            spins = 0;
+        } else {
+            if (spins++ >= P.spin_limit) {
+                raise_timeout(P.err);  // the compute wave it feeds then gives up
+                return;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+}
+
+// The converter wave of band w: per group, once its compute wave has staged it, p 2^e of
+// every cell to R (fp32) in the R table, and out[p] = R[N-1, M-1] as stored.
+SDTW_DEV void lin_convert_wave(const DPParams& P, const Smem& sm, int p, int g, int w) {
+    const int l = threadIdx.x & (WAVE - 1);
+    const int W = P.W, nb = P.nb, N = P.N, M = P.M, S = P.S;
+    const int b = g * W + w;
+    const int i = b * WAVE + l;
+    const double ngamma = -P.gamma;
+    const double* tabL = sm.tables() + fm::kExpTabN;
+    const bool out_lds = (b + 1 < nb) && (w + 1 < W);
+    const double* ring_p = reinterpret_cast<const double*>(sm.ring()) + (w + 1) * RS;
+    const int* ring_e = lin_ering(sm) + (w + 1) * RS;
+    const int* staged = sm.lin_staged() + w;
+    int* done = sm.lin_done() + w;
+    float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
+    const int s_out = i == N - 1 ? M - 1 + l : -1;  // this lane's step of cell (N-1, M-1)
+    int known = 0;
+    for (int s0 = 0; s0 < S; s0 += U) {
+        const int gi = s0 / U;
+        if (!wait_at_least(staged, gi + 1, known, P.err, P.spin_limit)) return;
+        const int k = gi & 1;
+        const bool edge = out_lds && l == WAVE - 1;
+        const double* sp = edge ? ring_p + hslot(s0 - (WAVE - 1)) : lin_stage_p(sm, w, k) + l * kLinRow;
+        const int* se = edge ? ring_e + hslot(s0 - (WAVE - 1)) : lin_stage_e(sm, w, k) + l * kLinRow;
+        double pv[U];
+        int ev[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            pv[u] = sp[u];
+            ev[u] = se[u];
+        }
+        // the reads are performed before this store (one LDS order per CU, a wave's in
+        // issue order), so the compute wave may then reuse the buffer
+        if (l == 0) lds_publish(done, gi + 1);
+        // all U conversions as one straight-line block (their table reads and chains
+        // interleave), then the stores, and out[p] by the one lane that holds it
+        float rv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) rv[u] = (float)lin_to_R(pv[u], ev[u], ngamma, tabL);
+        float* Rg = Rt + (int64_t)s0 * WAVE;
+#pragma unroll
+        for (int u = 0; u < U; ++u) Rg[u * WAVE] = rv[u];
+        if ((unsigned)(s_out - s0) < (unsigned)U) {
+            float ro = rv[0];
+#pragma unroll
+            for (int u = 1; u < U; ++u) ro = s_out - s0 == u ? rv[u] : ro;
+            P.out[p] = ro;
+        }
+    }
+}
+
+// Wave roles of a launch that can take the linear domain (W <= 2): compute waves 0 .. W-1,
+// producers W .. 2W-1, the helper 2W, converters 3 (W = 1) or 6, 7 (W = 2; wave 5 idle),
+// so that each compute wave keeps a SIMD to itself.  Every wave calls lin_pair_ok first.
+template <class Cost>
+SDTW_DEV void fwd_lin_roles(const DPParams& P, const Smem& sm, int p, int g, int w) {
+    const bool lin = lin_pair_ok(P, sm, p);
+    const int W = P.W;
+    if (w == 2 * W) {
+        if (g > 0) {
+            const int64_t row = (int64_t)p * P.G + (g - 1);
+            if (lin) helper_wave_lin(P, sm, reinterpret_cast<const double2*>(P.gring) + row * P.RW + RPAD);
+            else helper_wave(P, sm, P.gring + row * fwd_row_pitch(P) + RPAD, 0);
+        }
+        return;
+    }
+    const int conv0 = W == 1 ? 3 : 6;
+    if (w >= conv0) {
+        const int wb = w - conv0;
+        if (lin && g * W + wb < P.nb) lin_convert_wave(P, sm, p, g, wb);
+        return;
+    }
+    if (w > 2 * W) return;
+    const int wb = w >= W ? w - W : w;
+    if (g * W + wb >= P.nb) return;
+    if (w >= W) {
+        if (P.K != KXOf<Cost>::value) producer_wave<Cost, false>(P, sm, p, g * W + wb, wb);
+        else if (P.D_out) producer_wave<Cost, false, false, true, true>(P, sm, p, g * W + wb, wb);
+        else producer_wave<Cost, false, false, false, true>(P, sm, p, g * W + wb, wb);
+        return;
+    }
+    CostRing cost;
+    cost.bind(sm, w, P);
+    if (lin) fwd_band_lin(P, cost, sm, p, g, w);
+    else fwd_band<CostRing, false, true>(P, cost, sm, p, g, w);
+}
+
 template <class Cost, bool BWD>
 constexpr int dp_threads() { return Produced<Cost, BWD>::value ? 9 * WAVE : 5 * WAVE; }
 
-template <class Cost, bool BAND, bool EXACT>
-__global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPParams P) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    __shared__ __align__(16) double tab[kTabBytesFwd / 8];
-    Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W), kTabBytesFwd, tab};
+// The forward kernels' body.  LIN: a launch that can take the scaled linear domain (exact
+// arithmetic, matrix-core costs, no band, P.lin set by the host, W <= 2; fwd_lin_roles).
+template <class Cost, bool BAND, bool EXACT, bool LIN>
+SDTW_DEV void fwd_body(const DPParams& P, unsigned char* smem_raw, double* tab) {
+    static_assert(!LIN || (Produced<Cost, false>::value && !BAND && EXACT), "linear domain");
+    Smem sm{smem_raw, P.W, ring_bytes_fwd(P.W) + (LIN ? lin_extra_bytes(P.W) : 0), kTabBytesFwd, tab};
     // wave-uniform values are moved to scalar registers so that the branches on band,
     // group and pair compile to scalar branches, not exec-masked regions
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -1281,6 +1752,7 @@ __global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPPara
     if (threadIdx.x < 8) {
         sm.poison_in()[threadIdx.x] = 0;
         sm.bad_col()[threadIdx.x] = INT_MAX;
+        if (LIN) sm.lin_staged()[threadIdx.x] = 0;  // with lin_done and lin_red
     }
     sm.load_tables();
     // ring 0 starts at +inf: the padding row above band 0 (the helper wave overwrites it
@@ -1289,27 +1761,48 @@ __global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPPara
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
     const int p = t / P.G, g = t - p * P.G;
-    if (w == (Produced<Cost, false>::value ? 2 * P.W : P.W)) {
-        // helper wave: the previous workgroup's last row into ring 0
-        if (g > 0) helper_wave(P, sm, P.gring + ((int64_t)p * P.G + (g - 1)) * P.RW + RPAD, 0);
-        return;
-    }
-    if constexpr (Produced<Cost, false>::value) {
-        const int wb = w >= P.W ? w - P.W : w;  // band of this compute or producer wave
-        if (g * P.W + wb >= P.nb) return;
-        if (w >= P.W) {
-            producer_wave<Cost, false>(P, sm, p, g * P.W + wb, wb);
-        } else {
-            CostRing cost;
-            cost.bind(sm, w, P);
-            fwd_band<CostRing, BAND, EXACT>(P, cost, sm, p, g, w);
-        }
+    if constexpr (LIN) {
+        fwd_lin_roles<Cost>(P, sm, p, g, w);
     } else {
-        if (g * P.W + w >= P.nb) return;
-        Cost cost;
-        cost.init(P, p, g * P.W + w);
-        fwd_band<Cost, BAND, EXACT>(P, cost, sm, p, g, w);
+        if (w == (Produced<Cost, false>::value ? 2 * P.W : P.W)) {
+            // helper wave: the previous workgroup's last row into ring 0
+            if (g > 0) helper_wave(P, sm, P.gring + ((int64_t)p * P.G + (g - 1)) * fwd_row_pitch(P) + RPAD, 0);
+            return;
+        }
+        if constexpr (Produced<Cost, false>::value) {
+            const int wb = w >= P.W ? w - P.W : w;  // band of this compute or producer wave
+            if (g * P.W + wb >= P.nb) return;
+            if (w >= P.W) {
+                producer_wave<Cost, false>(P, sm, p, g * P.W + wb, wb);
+            } else {
+                CostRing cost;
+                cost.bind(sm, w, P);
+                fwd_band<CostRing, BAND, EXACT>(P, cost, sm, p, g, w);
+            }
+        } else {
+            if (g * P.W + w >= P.nb) return;
+            Cost cost;
+            cost.init(P, p, g * P.W + w);
+            fwd_band<Cost, BAND, EXACT>(P, cost, sm, p, g, w);
+        }
     }
+}
+
+template <class Cost, bool BAND, bool EXACT>
+__global__ void __launch_bounds__((dp_threads<Cost, false>())) fwd_kernel(DPParams P) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ __align__(16) double tab[kTabBytesFwd / 8];
+    fwd_body<Cost, BAND, EXACT, false>(P, smem_raw, tab);
+}
+
+// The linear-domain launch: at most 8 waves (fwd_lin_roles), so each may hold 256 VGPRs
+// (the producer's two tiles of operands in flight and the store addresses then fit without
+// reusing the registers of outstanding loads).
+template <class Cost>
+__global__ void __launch_bounds__(8 * WAVE) fwd_lin_kernel(DPParams P) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ __align__(16) double tab[kTabBytesFwd / 8];
+    fwd_body<Cost, false, true, true>(P, smem_raw, tab);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1540,11 +2033,6 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         if (!group(q0, std::false_type{})) return give_up_bwd(P, p, b);
 }
 
-template <class C>
-struct KXOf : std::integral_constant<int, 0> {};
-template <int KX>
-struct KXOf<CostMfma<KX>> : std::integral_constant<int, KX> {};
-
 // GW > 0: gradient mode for workgroups of up to GW bands.  GW = 2: waves compute 0 .. W-1,
 // producers W .. 2W-1, dL/dy waves 2W .. 3W-1, dL/dx waves 3W .. 4W-1, helper 4W (under
 // round-robin placement with W = 2 the dL/dy waves share the compute waves' SIMDs and the
@@ -1619,7 +2107,7 @@ bwd_kernel(DPParams P) {
 hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st);
 
 inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
-    const size_t ring = bwd ? ring_bytes_bwd(P.W) : ring_bytes_fwd(P.W);
+    const size_t ring = bwd ? ring_bytes_bwd(P.W) : ring_bytes_fwd(P.W) + (P.lin ? lin_extra_bytes(P.W) : 0);
     return 256 + ring + (size_t)P.W * WAVE * CS * sizeof(float);  // the tables are static
 }
 
@@ -1636,7 +2124,10 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipSt
     if (e != hipSuccess) return e;
     // one wave per band, plus a helper wave when a pair spans several workgroups; with
     // matrix-core costs, the helper slot and one producer wave per band
-    const int waves = grad ? (P.W <= 2 ? 4 : 3) * P.W + 1 : (produced ? 2 * P.W + 1 : P.W + (P.G > 1 ? 1 : 0));
+    // (a launch that can take the linear domain: a converter wave per band, fwd_lin_roles)
+    const int waves = grad ? (P.W <= 2 ? 4 : 3) * P.W + 1
+                      : !bwd && P.lin ? (P.W == 1 ? 4 : 8)
+                      : (produced ? 2 * P.W + 1 : P.W + (P.G > 1 ? 1 : 0));
     hipLaunchKernelGGL(kernel, dim3(P.B * P.G), dim3(waves * WAVE), lds, st, P);
     return hipGetLastError();
 }
@@ -1647,8 +2138,14 @@ hipError_t launch_cost(const DPParams& P, hipStream_t st) {
         if (P.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT>, P, true, Produced<Cost, true>::value, st);
         return launch_dp(bwd_kernel<Cost, false, EXACT>, P, true, Produced<Cost, true>::value, st);
     } else {
-        if (P.bw > 0.0) return launch_dp(fwd_kernel<Cost, true, EXACT>, P, false, Produced<Cost, false>::value, st);
-        return launch_dp(fwd_kernel<Cost, false, EXACT>, P, false, Produced<Cost, false>::value, st);
+        // the linear domain only where the kernel can take it
+        DPParams Q = P;
+        if (P.bw > 0.0 || !EXACT || !Produced<Cost, false>::value || P.W > 2) Q.lin = 0;
+        if constexpr (EXACT && Produced<Cost, false>::value) {
+            if (Q.lin) return launch_dp(fwd_lin_kernel<Cost>, Q, false, true, st);
+        }
+        if (Q.bw > 0.0) return launch_dp(fwd_kernel<Cost, true, EXACT>, Q, false, Produced<Cost, false>::value, st);
+        return launch_dp(fwd_kernel<Cost, false, EXACT>, Q, false, Produced<Cost, false>::value, st);
     }
 }
 

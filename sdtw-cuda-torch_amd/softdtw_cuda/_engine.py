@@ -376,22 +376,23 @@ def fused_costs_on_matrix_cores(N: int, M: int, K: int) -> bool:
 
 
 def fused_bands_per_workgroup(B: int, N: int, M: int, K: int, device) -> int:
-    """The fused forward recursions' bands per workgroup at this shape on `device` (the
-    library's own choice, sdtw_fused_bands_per_workgroup): 2 or 4."""
+    """The fused forward recursions' bands per workgroup for an unbanded call at this shape
+    on `device` under the current arithmetic (the library's own choice,
+    sdtw_fused_bands_per_workgroup): 1, 2 or 4."""
     with torch.cuda.device(device):
         return int(load().sdtw_fused_bands_per_workgroup(B, N, M, K))
 
 
 def one_launch_unfused_forward(B: int, N: int, M: int, K: int, device) -> bool:
     """Whether sdtw_fused_fwd_d_f32 beats the distance launch plus the D-reading recursion.
-    It needs matrix-core costs, and the library must take its 2-band geometry (the batch's
-    2-band workgroups all fit on the GPU at once): the producer waves then have SIMDs of
+    It needs matrix-core costs, and the library must take its 1- or 2-band geometry (the
+    batch's workgroups all fit on the GPU at once): the producer waves then have SIMDs of
     their own, whereas sharing their compute waves' SIMDs, the D stores slow the recursion
     (B=32 N=M=2048 D=64: 2.78 against 2.70 ms per step).  Not under "fast" arithmetic,
     whose short recursion step makes the storing producers the limit."""
     if not fused_costs_on_matrix_cores(N, M, K) or get_numerics() == "fast":
         return False
-    return fused_bands_per_workgroup(B, N, M, K, device) == 2
+    return fused_bands_per_workgroup(B, N, M, K, device) <= 2
 
 
 def fused_fwd_d(x, y, gamma: float, bandwidth: float):

@@ -165,27 +165,114 @@ def test_fused_feature_widths_match_unfused(K):
     assert torch.equal(E1, E2)
 
 
+def _linear_domain(B, N, M, K, bw):
+    """Whether the fused forward of this call takes the scaled linear-domain recursion:
+    exact or mixed arithmetic, no band, matrix-core costs, 1 or 2 bands per workgroup."""
+    return (_engine.get_numerics() != "fast" and not bw > 0
+            and _engine.fused_costs_on_matrix_cores(N, M, K)
+            and _engine.fused_bands_per_workgroup(B, N, M, K, "cuda") <= 2)
+
+
+def _oracle_R_check(R, D, gamma, bw, B, N, M):
+    """Against the CPU path on the same D: the share of the engine R table's cells with its
+    fp32 bits (both +inf counts as equal), the largest distance in fp32 ulps of the finite
+    ones (the same infinities required), and the CPU path's out."""
+    out_o, R_o = oracle.forward(D.cpu(), gamma, None if bw <= 0 else bw)
+    Rref = engine_R_from_oracle(R_o)
+    Rc = _engine.table_unpack(R, B, N, M).cpu()
+    same = (Rc == Rref) | (torch.isinf(Rc) & torch.isinf(Rref))
+    assert torch.equal(torch.isfinite(Rc), torch.isfinite(Rref))
+    fin = torch.isfinite(Rref)
+    ulps = (Rc[fin].view(torch.int32).long() - Rref[fin].view(torch.int32).long()).abs()
+    return same.double().mean().item(), int(ulps.max().item()) if ulps.numel() else 0, out_o
+
+
+# The scaled linear-domain forward evaluates the recursion more accurately than the CPU
+# path's log-domain form (a few gamma 2^-53 per cell against ulp(R)), so where the CPU path's
+# own fp64 rounding puts a cell next to an fp32 rounding boundary the two can round to
+# neighbouring floats: R within one fp32 ulp everywhere, with a few cells in 10^4 differing
+# on some inputs (none of the 8.4M at the headline shape).  The log-domain D-reading forward
+# shows such cells too, on other inputs.
+LIN_RATE = 0.999
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_fused_matches_unfused_kernels(mode):
-    # fused recomputes the same cost bits: identical out / R / E.  The last two shapes need
-    # more 2-band workgroups than the GPU has CUs, so the fused launch takes 4 bands per
-    # workgroup (producers sharing their compute waves' SIMDs), one of them with
-    # cross-workgroup boundaries and a partial last workgroup.
+    # fused recomputes the same cost bits.  Under fast arithmetic, and with a band, both run
+    # the same recursion: identical out / R / E.  Under exact and mixed arithmetic the fused
+    # forward of an unbanded call is the scaled linear-domain recursion and the D-reading one
+    # the log-domain form: each gives R with the CPU path's fp32 bits (bit-equal rate 1), and
+    # the fused backward equals the D-reading one on the same R.  The shapes with 300 and 70
+    # pairs need more 2-band workgroups than the GPU has CUs, so the fused launch takes 4
+    # bands per workgroup (the log-domain recursion, producers sharing their compute waves'
+    # SIMDs), one of them with cross-workgroup boundaries and a partial last workgroup.
     for (B, N, M, K, bw) in [(3, 50, 40, 5, -1.0), (2, 12, 9, 3, -1.0), (2, 1100, 300, 4, -1.0),
                              (300, 200, 150, 16, -1.0), (70, 600, 100, 8, -1.0),
                              (70, 600, 100, 8, 40.0), (2, 1, 7, 3, -1.0), (2, 7, 1, 3, -1.0),
                              (1, 65, 1, 2, -1.0)]:
-        say(f"[fused == unfused] mode={mode} B={B} N={N} M={M} K={K} bw={bw}")
+        say(f"[fused vs unfused] mode={mode} B={B} N={N} M={M} K={K} bw={bw}")
         x, y = randn_pair(B, N, M, K, seed=N)
         xg, yg = x.cuda(), y.cuda()
         with numerics(mode):
             D = _engine.sqeuclid_fwd(xg, yg)
             o1, R1 = _engine.dtw_fwd(D, 0.7, bw)
             o2, R2 = _engine.fused_fwd(xg, yg, 0.7, bw)
-            E1 = _engine.dtw_bwd(D, R1, 0.7, bw)
             E2 = _engine.fused_bwd_e(xg, yg, R2, 0.7, bw)
-        assert torch.equal(o1, o2) and torch.equal(R1, R2)
-        assert torch.equal(E1, E2)
+            E2d = _engine.dtw_bwd(D, R2, 0.7, bw)
+            lin = _linear_domain(B, N, M, K, bw)
+        assert torch.equal(E2, E2d)
+        if not lin:
+            assert torch.equal(o1, o2) and torch.equal(R1, R2)
+        else:
+            r1, u1, out_o = _oracle_R_check(R1, D, 0.7, bw, B, N, M)
+            r2, u2, _ = _oracle_R_check(R2, D, 0.7, bw, B, N, M)
+            say(f"    R vs CPU path: D-reading rate {r1:.8f} (max {u1} ulp), fused rate {r2:.8f} "
+                f"(max {u2} ulp)")
+            assert u1 <= 1 and r1 >= LIN_RATE and u2 <= 1 and r2 >= LIN_RATE
+            torch.testing.assert_close(o2.cpu(), out_o, rtol=FWD_RTOL, atol=0)
+
+
+@pytest.mark.parametrize("B,N,M,K,gamma,scale", [
+    (32, 512, 512, 64, 1.0, None),   # the headline shape: one band per workgroup
+    (64, 512, 128, 16, 0.5, None),   # 512 bands: two per workgroup (LDS and global handover)
+    (2, 150, 200, 8, 1.0, None),     # a partial last band
+    (2, 200, 180, 8, 0.05, None),    # sharp soft-min
+    (3, 70, 10, 4, 1.0, None),       # fewer columns than a group (no interior group)
+    (3, 200, 150, 8, 0.01, 300.0),   # pair 1 past the linear domain's bound: log domain
+    (3, 200, 150, 8, 1.0, "nan"),    # pair 2 with a NaN feature: log domain, NaN results
+])
+def test_linear_domain_forward_vs_oracle(B, N, M, K, gamma, scale):
+    # the fused forward's scaled linear-domain recursion (exact / mixed arithmetic, no band),
+    # against the CPU path's recursion on the same cost bits (the one-launch forward's D):
+    # R within one fp32 ulp, out to its tolerance; pairs whose norms fall outside the linear
+    # domain run the log-domain recursion in the same launch.  fused_fwd, which keeps no D,
+    # gives the same out and R.
+    say(f"[linear domain] B={B} N={N} M={M} K={K} gamma={gamma} scale={scale} "
+        f"bands/workgroup {_engine.fused_bands_per_workgroup(B, N, M, K, 'cuda')}")
+    x, y = randn_pair(B, N, M, K, seed=B + N + M)
+    if scale == "nan":
+        x[2, 5, 1] = float("nan")
+    elif scale is not None:
+        x[1] *= scale
+        y[1] *= scale
+    assert _linear_domain(B, N, M, K, -1.0)
+    out, R, Dg, _ = _engine.fused_fwd_d(x.cuda(), y.cuda(), gamma, -1.0)
+    out2, R2 = _engine.fused_fwd(x.cuda(), y.cuda(), gamma, -1.0)
+    torch.testing.assert_close(out2, out, rtol=0, atol=0, equal_nan=True)
+    torch.testing.assert_close(R2, R, rtol=0, atol=0, equal_nan=True)
+    out_o, R_o = oracle.forward(Dg.cpu(), gamma, None)
+    Rc = _engine.table_unpack(R, B, N, M).cpu()
+    Rref = engine_R_from_oracle(R_o)
+    nan = torch.isnan(Rref)
+    assert torch.equal(torch.isnan(Rc), nan)
+    same = (Rc == Rref) | (torch.isinf(Rc) & torch.isinf(Rref)) | nan
+    fin = torch.isfinite(Rref)
+    assert torch.equal(torch.isfinite(Rc), fin)
+    ulps = (Rc[fin].view(torch.int32).long() - Rref[fin].view(torch.int32).long()).abs()
+    rate = same.double().mean().item()
+    say(f"    R bit-equal rate {rate:.8f}, max {int(ulps.max())} ulp")
+    assert int(ulps.max()) <= 1 and rate >= LIN_RATE
+    torch.testing.assert_close(out.cpu(), out_o, rtol=FWD_RTOL, atol=0, equal_nan=True)
 
 
 @pytest.mark.parametrize("B,N,M,K,bw", [(3, 100, 80, 16, -1.0), (2, 130, 70, 64, 20.0),
@@ -199,7 +286,15 @@ def test_unfused_one_launch_forward_matches_two_calls(B, N, M, K, bw):
     D1 = _engine.sqeuclid_fwd(xg, yg)
     o1, R1 = _engine.dtw_fwd(D1, 0.7, bw)
     o2, R2, D2, rec = _engine.fused_fwd_d(xg, yg, 0.7, bw)
-    assert torch.equal(D1, D2) and torch.equal(R1, R2) and torch.equal(o1, o2)
+    assert torch.equal(D1, D2)
+    if not _linear_domain(B, N, M, K, bw):
+        assert torch.equal(R1, R2) and torch.equal(o1, o2)
+    else:
+        # the linear-domain recursion (unbanded, exact or mixed arithmetic)
+        r2, u2, out_o = _oracle_R_check(R2, D1, 0.7, bw, B, N, M)
+        say(f"    fused R vs CPU path: rate {r2:.8f}, max {u2} ulp")
+        assert u2 <= 1 and r2 >= LIN_RATE
+        torch.testing.assert_close(o2.cpu(), out_o, rtol=FWD_RTOL, atol=0)
     # the distance record: per pair 1 exactly where it holds a cost that is not positive,
     # then the row norms (256-byte aligned parts) with the norms kernel's bits
     cl = rec[:4 * B].view(torch.int32)

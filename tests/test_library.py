@@ -72,17 +72,25 @@ def test_workspace_sizes():
 
 def test_fused_geometry_query():
     # the library's own choice of bands per workgroup (without a visible GPU it assumes 256
-    # CUs, the MI355X count): 2 while the batch's 2-band workgroups all fit at once
+    # CUs, the MI355X count): 1 while the batch's one-band workgroups all fit at once under
+    # exact or mixed arithmetic (the linear-domain forward), else 2 while the 2-band ones fit
     q = _engine.load().sdtw_fused_bands_per_workgroup
-    assert q(32, 512, 512, 64) == 2      # 32 * 4 = 128 workgroups
-    assert q(32, 1024, 1024, 64) == 2    # 32 * 8 = 256: still fits
-    assert q(32, 2048, 2048, 64) == 4    # 32 * 16 = 512
-    assert q(16, 4096, 3072, 4) == 4     # the long configuration: 16 * 32 = 512
-    assert q(256, 64, 64, 8) == 2        # one band per pair
-    assert q(257, 64, 64, 8) == 4
-    assert q(4, 512, 512, 65) == 4       # K > 64: scalar cost tiles
-    assert q(1, 5, 5, 3) == 4            # K*N*M < 400: scalar cost tiles
-    assert q(1, 0, 5, 3) == 0            # invalid shape
+    prev = _engine.set_numerics("mixed")
+    try:
+        for mode in ("mixed", "exact", "fast"):
+            _engine.set_numerics(mode)
+            one = 1 if mode != "fast" else 2
+            assert q(32, 512, 512, 64) == one    # 32 * 8 = 256 one-band workgroups
+            assert q(32, 1024, 1024, 64) == 2    # 32 * 16 = 512; 32 * 8 = 256 2-band ones
+            assert q(32, 2048, 2048, 64) == 4    # 32 * 16 = 512 2-band ones
+            assert q(16, 4096, 3072, 4) == 4     # the long configuration: 16 * 32 = 512
+            assert q(256, 64, 64, 8) == one      # one band per pair
+            assert q(257, 64, 64, 8) == 4
+            assert q(4, 512, 512, 65) == 4       # K > 64: scalar cost tiles
+            assert q(1, 5, 5, 3) == 4            # K*N*M < 400: scalar cost tiles
+            assert q(1, 0, 5, 3) == 0            # invalid shape
+    finally:
+        _engine.set_numerics(prev)
 
 
 def test_one_launch_unfused_forward_choice(monkeypatch):
