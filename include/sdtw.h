@@ -130,7 +130,7 @@ int sdtw_set_deterministic(int on);
 /* Bands per workgroup the fused forward recursions (sdtw_fused_fwd_f32, sdtw_fused_fwd_d_f32)
  * take for an unbanded call at this shape on the current device under the current
  * arithmetic: 1 when the batch's one-band workgroups all fit on the GPU at once and the
- * arithmetic is exact or mixed (the scaled linear-domain recursion, whose compute, producer,
+ * arithmetic is mixed (the scaled linear-domain recursion, whose compute, producer,
  * helper and converter waves then have a SIMD each), else 2 when the 2-band workgroups all
  * fit (their matrix-core producer waves have SIMDs of their own), else 4; 0 for an invalid
  * shape.  (A banded call takes 2 where this is 1.)  The choice the launcher makes, exported

@@ -210,13 +210,16 @@ std::atomic<int> g_numerics{SDTW_NUMERICS_MIXED};
 // forward: fp64-accurate exp / log unless FAST; backward: only in EXACT
 bool exact_forward() { return g_numerics.load(std::memory_order_relaxed) != SDTW_NUMERICS_FAST; }
 bool exact_backward() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_EXACT; }
+// the fused forwards' scaled linear-domain recursion: mixed arithmetic only (exact keeps the
+// log-domain form, whose R carries the CPU path's fp32 bits)
+bool lin_forward() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_MIXED; }
 
 // The fused forward: one band per workgroup where the batch's one-band workgroups all fit
-// and the call takes the scaled linear-domain recursion (exact arithmetic, matrix-core
+// and the call takes the scaled linear-domain recursion (mixed arithmetic, matrix-core
 // costs, no band): its compute, producer, helper and converter waves then have a SIMD each.
 // Otherwise fused_wmax.
 int fused_fwd_wmax(int64_t B, int64_t N, int64_t M, int64_t K, double bandwidth) {
-    if (exact_forward() && !(bandwidth > 0.0) && fused_bwd_wmax(B, N, M, K) == 1) return 1;
+    if (lin_forward() && !(bandwidth > 0.0) && fused_bwd_wmax(B, N, M, K) == 1) return 1;
     return fused_wmax(B, N, M, K);
 }
 
@@ -488,9 +491,9 @@ static int fused_fwd_common(const float* x, const float* y, float* D, void* reco
     p.R = R;
     p.out = out;
     p.D_out = D;
-    // pairs whose norms allow it take the scaled linear-domain recursion (exact arithmetic,
+    // pairs whose norms allow it take the scaled linear-domain recursion (mixed arithmetic,
     // matrix-core costs, no band, up to 2 bands per workgroup)
-    p.lin = exact_forward() && !(p.bw > 0.0) && mfma_costs(N, M, K) && p.W <= 2 ? 1 : 0;
+    p.lin = lin_forward() && !(p.bw > 0.0) && mfma_costs(N, M, K) && p.W <= 2 ? 1 : 0;
     if (D && record) {  // the distance record: clamp flags, and the norms formed here
         const DistRecord rec = dist_record(record, B, N, M);
         p.clamped = rec.clamped;

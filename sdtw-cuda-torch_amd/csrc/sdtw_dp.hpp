@@ -1738,7 +1738,8 @@ template <class Cost, bool BWD>
 constexpr int dp_threads() { return Produced<Cost, BWD>::value ? 9 * WAVE : 5 * WAVE; }
 
 // The forward kernels' body.  LIN: a launch that can take the scaled linear domain (exact
-// arithmetic, matrix-core costs, no band, P.lin set by the host, W <= 2; fwd_lin_roles).
+// cell arithmetic, matrix-core costs, no band, P.lin set by the host for mixed arithmetic,
+// W <= 2; fwd_lin_roles).
 template <class Cost, bool BAND, bool EXACT, bool LIN>
 SDTW_DEV void fwd_body(const DPParams& P, unsigned char* smem_raw, double* tab) {
     static_assert(!LIN || (Produced<Cost, false>::value && !BAND && EXACT), "linear domain");

@@ -38,8 +38,9 @@ struct DPParams {
     int* err;           // spin-timeout flag
     unsigned spin_limit;  // polls a bounded wait makes before it gives up (kDefaultSpinLimit)
     int B, N, M, K;
-    int lin;            // forward, matrix-core costs, no band, W <= 2: pairs whose costs allow it
-                        // run the scaled linear-domain recursion (fwd_band_lin)
+    int lin;            // forward under mixed arithmetic, matrix-core costs, no band, W <= 2:
+                        // pairs whose costs allow it run the scaled linear-domain recursion
+                        // (fwd_band_lin)
     int nb, W, G;       // 64-row bands per pair, waves per workgroup, workgroups per pair
     int S;              // steps per band in the R table (dp_band_steps(M))
     double gamma, inv_gamma, bw;

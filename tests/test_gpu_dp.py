@@ -167,8 +167,8 @@ def test_fused_feature_widths_match_unfused(K):
 
 def _linear_domain(B, N, M, K, bw):
     """Whether the fused forward of this call takes the scaled linear-domain recursion:
-    exact or mixed arithmetic, no band, matrix-core costs, 1 or 2 bands per workgroup."""
-    return (_engine.get_numerics() != "fast" and not bw > 0
+    mixed arithmetic, no band, matrix-core costs, 1 or 2 bands per workgroup."""
+    return (_engine.get_numerics() == "mixed" and not bw > 0
             and _engine.fused_costs_on_matrix_cores(N, M, K)
             and _engine.fused_bands_per_workgroup(B, N, M, K, "cuda") <= 2)
 
@@ -198,11 +198,11 @@ LIN_RATE = 0.999
 
 @pytest.mark.parametrize("mode", MODES)
 def test_fused_matches_unfused_kernels(mode):
-    # fused recomputes the same cost bits.  Under fast arithmetic, and with a band, both run
-    # the same recursion: identical out / R / E.  Under exact and mixed arithmetic the fused
+    # fused recomputes the same cost bits.  Under exact and fast arithmetic, and with a band,
+    # both run the same recursion: identical out / R / E.  Under mixed arithmetic the fused
     # forward of an unbanded call is the scaled linear-domain recursion and the D-reading one
-    # the log-domain form: each gives R with the CPU path's fp32 bits (bit-equal rate 1), and
-    # the fused backward equals the D-reading one on the same R.  The shapes with 300 and 70
+    # the log-domain form: each gives R within one fp32 ulp of the CPU path's, and the fused
+    # backward equals the D-reading one on the same R.  The shapes with 300 and 70
     # pairs need more 2-band workgroups than the GPU has CUs, so the fused launch takes 4
     # bands per workgroup (the log-domain recursion, producers sharing their compute waves'
     # SIMDs), one of them with cross-workgroup boundaries and a partial last workgroup.
@@ -242,7 +242,7 @@ def test_fused_matches_unfused_kernels(mode):
     (3, 200, 150, 8, 1.0, "nan"),    # pair 2 with a NaN feature: log domain, NaN results
 ])
 def test_linear_domain_forward_vs_oracle(B, N, M, K, gamma, scale):
-    # the fused forward's scaled linear-domain recursion (exact / mixed arithmetic, no band),
+    # the fused forward's scaled linear-domain recursion (mixed arithmetic, no band),
     # against the CPU path's recursion on the same cost bits (the one-launch forward's D):
     # R within one fp32 ulp, out to its tolerance; pairs whose norms fall outside the linear
     # domain run the log-domain recursion in the same launch.  fused_fwd, which keeps no D,

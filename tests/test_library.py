@@ -73,13 +73,13 @@ def test_workspace_sizes():
 def test_fused_geometry_query():
     # the library's own choice of bands per workgroup (without a visible GPU it assumes 256
     # CUs, the MI355X count): 1 while the batch's one-band workgroups all fit at once under
-    # exact or mixed arithmetic (the linear-domain forward), else 2 while the 2-band ones fit
+    # mixed arithmetic (the linear-domain forward), else 2 while the 2-band ones fit
     q = _engine.load().sdtw_fused_bands_per_workgroup
     prev = _engine.set_numerics("mixed")
     try:
         for mode in ("mixed", "exact", "fast"):
             _engine.set_numerics(mode)
-            one = 1 if mode != "fast" else 2
+            one = 1 if mode == "mixed" else 2
             assert q(32, 512, 512, 64) == one    # 32 * 8 = 256 one-band workgroups
             assert q(32, 1024, 1024, 64) == 2    # 32 * 16 = 512; 32 * 8 = 256 2-band ones
             assert q(32, 2048, 2048, 64) == 4    # 32 * 16 = 512 2-band ones
