@@ -463,7 +463,9 @@ struct CostMfma {
         const int l = threadIdx.x & (WAVE - 1);
         const int sl = (c0 + (l & 15)) & (CR - 1);
         float* dst = ring + 4 * (l >> 4) * CS + sl;
-        const bool mir = sl < U;  // the mirror slots
+        // the mirror slots (sl < U) take a second copy; the other lanes store their value
+        // to the same slot again, so the stores need no branch
+        float* dst2 = sl < U ? dst + CR : dst;
         float sum = 0.0f;
         float mn = __builtin_inff();
 #pragma unroll
@@ -472,7 +474,7 @@ struct CostMfma {
             for (int r = 0; r < 4; ++r) {
                 const float v = clamp0(exact_cost_pre(x2o[rb][r], y2c, acc[rb][r]));
                 dst[(16 * rb + r) * CS] = v;
-                if (mir) dst[(16 * rb + r) * CS + CR] = v;
+                dst2[(16 * rb + r) * CS] = v;
                 sum += v;
                 mn = (v > 0.0f) ? fminf(mn, v) : 0.0f;  // NaN or 0 -> 0
             }
@@ -1484,7 +1486,6 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
         if (b == 0) return true;
         const bool live = c0 < M;
         const int need = min(c0 + U, M);
-        known_in = max(known_in, __builtin_amdgcn_readfirstlane(lds_load(in_flag)));
         if (live && known_in < need && !wait_at_least(in_flag, need, known_in, P.err, P.spin_limit))
             return false;
         __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the ring reads stay after the count
@@ -1524,6 +1525,18 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
         constexpr bool INTERIOR = decltype(interior_tag)::value;
 #pragma unroll
         for (int u = 0; u < U; ++u) d_cur[u] = d_nxt[u];
+        // the counters this group start checks, loaded together (one LDS round trip; each
+        // wait below then polls only if its cached count falls short)
+        {
+            const int v_ready = lds_load(cost.ready);
+            const int v_in = lds_load(in_flag);
+            const int v_conv = lds_load(conv);
+            const int v_free = lds_load(sm.cons() + (w + 1));
+            cost.known = max(cost.known, __builtin_amdgcn_readfirstlane(v_ready));
+            known_in = max(known_in, __builtin_amdgcn_readfirstlane(v_in));
+            known_conv = max(known_conv, __builtin_amdgcn_readfirstlane(v_conv));
+            known_free = max(known_free, __builtin_amdgcn_readfirstlane(v_free));
+        }
         if (!cost.begin(cring, s0 + 2 * TC) || !fetch(s0)) return -1;
         if (out_lds) {
             const int need_free = s0 + U - WAVE + 1 - RS;
@@ -1956,6 +1969,16 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         for (int u = 0; u < U; ++u) {
             r_cur[u] = r_nxt[u];
             d_cur[u] = d_nxt[u];
+        }
+        // the counters this group start checks, loaded together (one LDS round trip; each
+        // wait below then polls only if its cached count falls short)
+        {
+            const int v_in = lds_load(lin_flag);
+            const int v_free = lds_load(sm.cons() + w);
+            if constexpr (std::is_same<Cost, CostRing>::value)
+                cost.known = max(cost.known, __builtin_amdgcn_readfirstlane(lds_load(cost.ready)));
+            known_in = max(known_in, __builtin_amdgcn_readfirstlane(v_in));
+            known_free = max(known_free, __builtin_amdgcn_readfirstlane(v_free));
         }
         if (!cost.begin(cring, tile_col(q0 + 2 * TC)) || !fetch_lds(q0, dn_cur)) return false;
         const int n0 = q0 + U;
