@@ -1461,7 +1461,6 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
     const int* in_e = ering + w * RS;
     double* out_p = pring + (w + 1) * RS;
     int* out_e = ering + (w + 1) * RS;
-    double2* gout = reinterpret_cast<double2*>(P.gring) + ((int64_t)p * G + g) * P.RW + RPAD;
     const int* in_flag = sm.prod() + w;
     int* staged = sm.lin_staged() + w;
     const int* conv = sm.lin_done() + w;
@@ -1520,7 +1519,8 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
     // One group of U steps from s0 (pipeline as fwd_band's).  Each step's values go to the
     // lane's row of the converter stage (buffer (s0 / U) & 1), except lane 63's when a band
     // of this workgroup is below: those go to the handoff ring, where the converter reads
-    // them too.  INTERIOR: every lane inside the table for all U steps (no masking).
+    // them too.  A band below in the next workgroup gets them from the converter.
+    // INTERIOR: every lane inside the table for all U steps (no masking).
     auto group = [&](int s0, auto interior_tag) -> int {
         constexpr bool INTERIOR = decltype(interior_tag)::value;
 #pragma unroll
@@ -1583,16 +1583,9 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
         }
         cost.end(cring, s0 + 2 * TC, s0 + 3 * TC);
         if (l == 0) lds_publish(staged, gi + 1);
-        if (out_lds) {
-            if (l == WAVE - 1) lds_publish(sm.prod() + (w + 1), min(max(s0 + U - (WAVE - 1), 0), M));
-        } else if (out_glb && l >= WAVE - U) {
-            // lane 63's values of this group (columns s0 - 63 .. s0 - 48, inside the row's
-            // padding) from its stage row to the cross-workgroup row
-            const int u = l - (WAVE - U);
-            const double pv = lin_stage_p(sm, w, k)[(WAVE - 1) * kLinRow + u];
-            const int ev = lin_stage_e(sm, w, k)[(WAVE - 1) * kLinRow + u];
-            glb_put_lin(gout + (s0 - (WAVE - 1)) + u, pv, ev);
-        }
+        // (a band below in the next workgroup takes lane 63's values from the converter wave,
+        // which reads this stage anyway: lin_convert_wave)
+        if (out_lds && l == WAVE - 1) lds_publish(sm.prod() + (w + 1), min(max(s0 + U - (WAVE - 1), 0), M));
         return 0;
     };
 
@@ -1661,15 +1654,20 @@ SDTW_DEV void helper_wave_lin(const DPParams& P, const Smem& sm, const double2* 
 }
 
 // The converter wave of band w: per group, once its compute wave has staged it, p 2^e of
-// every cell to R (fp32) in the R table, and out[p] = R[N-1, M-1] as stored.
+// every cell to R (fp32) in the R table, and out[p] = R[N-1, M-1] as stored.  For a band
+// with a band below in the next workgroup it also copies lane 63's staged values of the
+// group (columns s0 - 63 .. s0 - 48, inside the row's padding) to the workgroup's
+// cross-workgroup row, off the compute wave.
 SDTW_DEV void lin_convert_wave(const DPParams& P, const Smem& sm, int p, int g, int w) {
     const int l = threadIdx.x & (WAVE - 1);
-    const int W = P.W, nb = P.nb, N = P.N, M = P.M, S = P.S;
+    const int W = P.W, G = P.G, nb = P.nb, N = P.N, M = P.M, S = P.S;
     const int b = g * W + w;
     const int i = b * WAVE + l;
     const double ngamma = -P.gamma;
     const double* tabL = sm.tables() + fm::kExpTabN;
     const bool out_lds = (b + 1 < nb) && (w + 1 < W);
+    const bool out_glb = (b + 1 < nb) && (w + 1 == W);
+    double2* gout = reinterpret_cast<double2*>(P.gring) + ((int64_t)p * G + g) * P.RW + RPAD;
     const double* ring_p = reinterpret_cast<const double*>(sm.ring()) + (w + 1) * RS;
     const int* ring_e = lin_ering(sm) + (w + 1) * RS;
     const int* staged = sm.lin_staged() + w;
@@ -1691,9 +1689,15 @@ SDTW_DEV void lin_convert_wave(const DPParams& P, const Smem& sm, int p, int g, 
             pv[u] = sp[u];
             ev[u] = se[u];
         }
+        // lanes 48 .. 63: lane 63's value of step s0 + l - 48, for the cross-workgroup row
+        const int hu = l - (WAVE - U);
+        const bool ho = out_glb && hu >= 0;
+        const double hp = lin_stage_p(sm, w, k)[(WAVE - 1) * kLinRow + (hu & (U - 1))];
+        const int he = lin_stage_e(sm, w, k)[(WAVE - 1) * kLinRow + (hu & (U - 1))];
         // the reads are performed before this store (one LDS order per CU, a wave's in
         // issue order), so the compute wave may then reuse the buffer
         if (l == 0) lds_publish(done, gi + 1);
+        if (ho) glb_put_lin(gout + (s0 - (WAVE - 1)) + hu, hp, he);
         // all U conversions as one straight-line block (their table reads and chains
         // interleave), then the stores, and out[p] by the one lane that holds it
         float rv[U];
