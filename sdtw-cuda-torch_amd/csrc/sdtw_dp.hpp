@@ -659,6 +659,8 @@ struct Smem {
     SDTW_DEV int* lin_staged() const { return reinterpret_cast<int*>(base) + 56; }
     SDTW_DEV int* lin_done() const { return reinterpret_cast<int*>(base) + 58; }
     SDTW_DEV unsigned* lin_red() const { return reinterpret_cast<unsigned*>(base) + 60; }
+    // groups whose cost exponentials the exponential wave has staged (W = 1; int 63)
+    SDTW_DEV int* lin_pdready() const { return reinterpret_cast<int*>(base) + 63; }
     SDTW_DEV double* tables() const { return tab; }
     SDTW_DEV unsigned char* ring() const { return base + 256; }
     SDTW_DEV float* cost_ring(int w) const {
@@ -1073,7 +1075,12 @@ SDTW_HD size_t ring_bytes_bwd(int W) { return (size_t)(W + 1) * RS * sizeof(floa
 constexpr int kLinNeg = -(1 << 30);  // exponent of a zero value (R = +inf)
 constexpr int kLinRow = U + 1;
 constexpr int kLinBuf = WAVE * kLinRow;
-SDTW_HD size_t lin_extra_bytes(int W) { return (size_t)(W + 1) * RS * 4 + (size_t)W * 2 * kLinBuf * 12; }
+// (W = 1 adds the cost-exponential stage: kPdBufs buffers of 64 lane rows of kLinRow (pD,
+// eD), filled by the workgroup's exponential wave, lin_exp_wave)
+constexpr int kPdBufs = 3;
+SDTW_HD size_t lin_extra_bytes(int W) {
+    return (size_t)(W + 1) * RS * 4 + (size_t)W * 2 * kLinBuf * 12 + (W == 1 ? (size_t)kPdBufs * kLinBuf * 12 : 0);
+}
 SDTW_DEV int* lin_ering(const Smem& sm) { return reinterpret_cast<int*>(sm.ring() + ring_bytes_fwd(sm.W)); }
 SDTW_DEV double* lin_stage_p(const Smem& sm, int w, int k) {
     return reinterpret_cast<double*>(lin_ering(sm) + (sm.W + 1) * RS) + (w * 2 + k) * kLinBuf;
@@ -1081,6 +1088,10 @@ SDTW_DEV double* lin_stage_p(const Smem& sm, int w, int k) {
 SDTW_DEV int* lin_stage_e(const Smem& sm, int w, int k) {
     return reinterpret_cast<int*>(lin_stage_p(sm, sm.W, 0)) + (w * 2 + k) * kLinBuf;
 }
+SDTW_DEV double* lin_pd_p(const Smem& sm, int k) {
+    return reinterpret_cast<double*>(lin_stage_e(sm, sm.W, 0)) + k * kLinBuf;
+}
+SDTW_DEV int* lin_pd_e(const Smem& sm, int k) { return reinterpret_cast<int*>(lin_pd_p(sm, kPdBufs)) + k * kLinBuf; }
 // Cross-workgroup rows of the forward: 8-byte entries (R), or in a launch that can take the
 // linear domain 16-byte ones, (p, then e and the tag 1), written and read as two 64-bit
 // halves, each whole or empty.  All rows of such a launch are 16-byte pitched, so the rows
@@ -1443,7 +1454,9 @@ SDTW_DEV bool lin_pair_ok(const DPParams& P, const Smem& sm, int p) {
            (double)(P.N + P.M + 2) * (xmax * 1.4426950408889634 + 4.0) < 536870912.0;
 }
 
-template <class Cost>
+// PD: the cost exponentials come staged from the workgroup's exponential wave (W = 1)
+// rather than from the compute wave's own evaluation of the cost ring.
+template <bool PD, class Cost>
 SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p, int g, int w) {
     const int l = threadIdx.x & (WAVE - 1);
     const int W = P.W, G = P.G, nb = P.nb, N = P.N, M = P.M, S = P.S;
@@ -1464,8 +1477,10 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
     const int* in_flag = sm.prod() + w;
     int* staged = sm.lin_staged() + w;
     const int* conv = sm.lin_done() + w;
+    const int* pdready = sm.lin_pdready();
+    const int groups = S / U;
 
-    int known_in = 0, known_free = 0, known_conv = 0;
+    int known_in = 0, known_free = 0, known_conv = 0, known_pd = 0;
     double lp = 0.0;  // this lane's value one step ago (its left; lane l+1's up by DPP)
     int le = kLinNeg;
     double dp = (b == 0 && l == 0) ? 1.0 : 0.0;  // diagonal: R[0,0] = 0 above-left of cell (0, 0)
@@ -1532,6 +1547,8 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
             const int v_in = lds_load(in_flag);
             const int v_conv = lds_load(conv);
             const int v_free = lds_load(sm.cons() + (w + 1));
+            const int v_pd = PD ? lds_load(pdready) : 0;
+            known_pd = max(known_pd, __builtin_amdgcn_readfirstlane(v_pd));
             cost.known = max(cost.known, __builtin_amdgcn_readfirstlane(v_ready));
             known_in = max(known_in, __builtin_amdgcn_readfirstlane(v_in));
             known_conv = max(known_conv, __builtin_amdgcn_readfirstlane(v_conv));
@@ -1546,7 +1563,12 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
         // the stage buffer of this group was last read by the converter for group gi - 2
         const int gi = s0 / U;
         if (gi >= 2 && !wait_at_least(conv, gi - 1, known_conv, P.err, P.spin_limit)) return -1;
+        // the exponentials of this group and the next are staged (the next ones before this
+        // group can finish: the producer may then reuse the cost slots they were read from)
+        if (PD && !wait_at_least(pdready, min(gi + 2, groups), known_pd, P.err, P.spin_limit)) return -1;
         const int k = gi & 1;
+        const double* pdp = lin_pd_p(sm, gi % kPdBufs) + l * kLinRow;
+        const int* pde = lin_pd_e(sm, gi % kPdBufs) + l * kLinRow;
         const bool edge = out_lds && l == WAVE - 1;
         double* sp = edge ? out_p + hslot(s0 - (WAVE - 1)) : lin_stage_p(sm, w, k) + l * kLinRow;
         int* se = edge ? out_e + hslot(s0 - (WAVE - 1)) : lin_stage_e(sm, w, k) + l * kLinRow;
@@ -1555,7 +1577,12 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
         for (int u = 0; u < U; ++u) {
             double pD;
             int eD;
-            lin_cost(d_cur[u], ninv_gamma, tabE, pD, eD);
+            if constexpr (PD) {
+                pD = pdp[u];
+                eD = pde[u];
+            } else {
+                lin_cost(d_cur[u], ninv_gamma, tabE, pD, eD);
+            }
             const double upp = shr1(up_p[u], lp);
             const int upe = dpp_shr1(up_e[u], le);
             const int em = max(max(upe, le), de);
@@ -1578,7 +1605,7 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
             le = en;
             sp[u] = q;
             se[u] = en;
-            d_nxt[u] = dn[u];
+            if constexpr (!PD) d_nxt[u] = dn[u];
             cost.step(u, s0 + 2 * TC, s0 + 3 * TC);
         }
         cost.end(cring, s0 + 2 * TC, s0 + 3 * TC);
@@ -1591,7 +1618,7 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
 
     if (!cost.prologue(cring, 0) || !cost.prologue(cring, TC)) return give_up_fwd(P, p);
     cost.preload(2 * TC);
-    {
+    if constexpr (!PD) {
         const float* dn = crow + ((-l) & (CR - 1));
 #pragma unroll
         for (int u = 0; u < U; ++u) d_nxt[u] = dn[u];
@@ -1608,6 +1635,45 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
         if (group(s0, T_{}) != 0) return give_up_fwd(P, p);
     for (; s0 < S; s0 += U)
         if (group(s0, F_{}) != 0) return give_up_fwd(P, p);
+}
+
+// The exponential wave of a one-band workgroup (W = 1): for each group h of the band, the
+// cost exponentials exp(-d / gamma) = pD 2^eD of its cells (lane l's row of the cost ring,
+// as the compute wave would read them) into stage buffer h mod 3, counted in lin_pdready.
+// Group h's costs are in the ring once tiles 0 .. h are (ready >= h + 1); buffer h mod 3 is
+// free once the compute wave has finished group h - 3 (done >= h - 2), so the wave works up
+// to two groups ahead.  The compute wave waits for group g + 1's exponentials before it
+// starts group g, so they are read before it finishes group g, after which the producer
+// may reuse the oldest of their slots.
+SDTW_DEV void lin_exp_wave(const DPParams& P, const Smem& sm, int w) {
+    const int l = threadIdx.x & (WAVE - 1);
+    const int groups = P.S / U;
+    const double ninv_gamma = -P.inv_gamma;
+    const double* tabE = sm.tables();
+    const float* crow = sm.cost_ring(w) + l * CS;
+    const int* ready = sm.ready() + w;
+    const int* done = sm.done() + w;
+    int* pdready = sm.lin_pdready();
+    int known_r = 0, known_d = 0;
+    for (int h = 0; h < groups; ++h) {
+        if (!wait_at_least(ready, h + 1, known_r, P.err, P.spin_limit)) return;
+        if (h >= kPdBufs && !wait_at_least(done, h - (kPdBufs - 1), known_d, P.err, P.spin_limit)) return;
+        double* pp = lin_pd_p(sm, h % kPdBufs) + l * kLinRow;
+        int* pe = lin_pd_e(sm, h % kPdBufs) + l * kLinRow;
+        const float* dn = crow + ((h * U - l) & (CR - 1));  // U consecutive slots (mirrored)
+        float d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) d[u] = dn[u];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            double pD;
+            int eD;
+            lin_cost(d[u], ninv_gamma, tabE, pD, eD);
+            pp[u] = pD;
+            pe[u] = eD;
+        }
+        if (l == 0) lds_publish(pdready, h + 1);
+    }
 }
 
 // The helper wave of a linear-domain pair: helper_wave for 16-byte (p, e) entries.
@@ -1717,7 +1783,8 @@ SDTW_DEV void lin_convert_wave(const DPParams& P, const Smem& sm, int p, int g, 
 
 // Wave roles of a launch that can take the linear domain (W <= 2): compute waves 0 .. W-1,
 // producers W .. 2W-1, the helper 2W, converters 3 (W = 1) or 6, 7 (W = 2; wave 5 idle),
-// so that each compute wave keeps a SIMD to itself.  Every wave calls lin_pair_ok first.
+// and with W = 1 the exponential wave 6 (waves 4, 5 idle), so that each compute wave keeps
+// a SIMD to itself under round-robin placement.  Every wave calls lin_pair_ok first.
 template <class Cost>
 SDTW_DEV void fwd_lin_roles(const DPParams& P, const Smem& sm, int p, int g, int w) {
     const bool lin = lin_pair_ok(P, sm, p);
@@ -1728,6 +1795,10 @@ SDTW_DEV void fwd_lin_roles(const DPParams& P, const Smem& sm, int p, int g, int
             if (lin) helper_wave_lin(P, sm, reinterpret_cast<const double2*>(P.gring) + row * P.RW + RPAD);
             else helper_wave(P, sm, P.gring + row * fwd_row_pitch(P) + RPAD, 0);
         }
+        return;
+    }
+    if (W == 1 && w >= 4) {
+        if (w == 6 && lin && g < P.nb) lin_exp_wave(P, sm, 0);
         return;
     }
     const int conv0 = W == 1 ? 3 : 6;
@@ -1747,7 +1818,8 @@ SDTW_DEV void fwd_lin_roles(const DPParams& P, const Smem& sm, int p, int g, int
     }
     CostRing cost;
     cost.bind(sm, w, P);
-    if (lin) fwd_band_lin(P, cost, sm, p, g, w);
+    if (lin && W == 1) fwd_band_lin<true>(P, cost, sm, p, g, w);
+    else if (lin) fwd_band_lin<false>(P, cost, sm, p, g, w);
     else fwd_band<CostRing, false, true>(P, cost, sm, p, g, w);
 }
 
@@ -2154,7 +2226,7 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipSt
     // matrix-core costs, the helper slot and one producer wave per band
     // (a launch that can take the linear domain: a converter wave per band, fwd_lin_roles)
     const int waves = grad ? (P.W <= 2 ? 4 : 3) * P.W + 1
-                      : !bwd && P.lin ? (P.W == 1 ? 4 : 8)
+                      : !bwd && P.lin ? (P.W == 1 ? 7 : 8)
                       : (produced ? 2 * P.W + 1 : P.W + (P.G > 1 ? 1 : 0));
     hipLaunchKernelGGL(kernel, dim3(P.B * P.G), dim3(waves * WAVE), lds, st, P);
     return hipGetLastError();
