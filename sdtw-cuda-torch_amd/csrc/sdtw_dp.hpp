@@ -737,7 +737,9 @@ struct GTile {
 // Gradient mode (GRAD, backward only): the band's gradient waves copy each G tile out of the
 // slots instead, counting the tiles in gdone (one count per gradient part); the producer
 // then waits for both counts >= t - 3 (which implies done >= t - 3) and stores no G tile.
-template <class Src, bool BWD, bool GRAD = false, bool DST = false, bool DB = false>
+// REC: set the pair's clamp record (P.clamped) where a tile holds a cost that is not
+// positive; with DB only where asked for (a wave other than the producer may store D).
+template <class Src, bool BWD, bool GRAD = false, bool DST = false, bool DB = false, bool REC = DST>
 SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int w) {
     constexpr bool MMA = !std::is_same<Src, CostD>::value;
     static_assert(!GRAD || (BWD && MMA), "gradient mode: fused backward only");
@@ -811,10 +813,11 @@ SDTW_DEV void producer_wave(const DPParams& P, const Smem& sm, int p, int b, int
         }
         // unfused mode's cost tensor, from the same tile (forward; after the next loads, so
         // that they do not queue behind these stores), and the pair's clamp record
-        // (DST: the stores are compiled in; without DB they follow P.D_out at run time)
+        // (DST: the stores are compiled in; without DB they follow P.D_out at run time; with DB,
+        // REC and not DST another wave stores D, lin_exp_wave, and only the record is set here)
         if constexpr (MMA && !BWD) {
-            if (DST || (!DB && P.D_out)) {
-                c.template store_d<DB>(P.D_out + (int64_t)p * P.N * P.M, col(t), b * WAVE, P.N);
+            if (DST || (!DB && P.D_out)) c.template store_d<DB>(P.D_out + (int64_t)p * P.N * P.M, col(t), b * WAVE, P.N);
+            if (REC || (!DB && P.D_out)) {
                 if (P.clamped && c.tile_nonpos && !clamp_marked) {
                     clamp_marked = true;
                     if ((threadIdx.x & (WAVE - 1)) == 0) P.clamped[p] = 1;
@@ -1645,12 +1648,20 @@ SDTW_DEV void fwd_band_lin(const DPParams& P, Cost& cost, const Smem& sm, int p,
 // to two groups ahead.  The compute wave waits for group g + 1's exponentials before it
 // starts group g, so they are read before it finishes group g, after which the producer
 // may reuse the oldest of their slots.
-SDTW_DEV void lin_exp_wave(const DPParams& P, const Smem& sm, int w) {
+// With STORE_D (the unfused one-launch forward) it also stores each cost tile h to D from
+// the ring, in the producer's coalesced layout (store_d's, entries past the table stored to
+// the last row / column, which receive their own bits again), taking the stores off the
+// producer.
+template <bool STORE_D>
+SDTW_DEV void lin_exp_wave(const DPParams& P, const Smem& sm, int p, int b, int w) {
     const int l = threadIdx.x & (WAVE - 1);
     const int groups = P.S / U;
+    const int N = P.N, M = P.M;
     const double ninv_gamma = -P.inv_gamma;
     const double* tabE = sm.tables();
-    const float* crow = sm.cost_ring(w) + l * CS;
+    const float* ring = sm.cost_ring(w);
+    const float* crow = ring + l * CS;
+    float* Dp = STORE_D ? P.D_out + (int64_t)p * N * M : nullptr;
     const int* ready = sm.ready() + w;
     const int* done = sm.done() + w;
     int* pdready = sm.lin_pdready();
@@ -1673,6 +1684,20 @@ SDTW_DEV void lin_exp_wave(const DPParams& P, const Smem& sm, int w) {
             pe[u] = eD;
         }
         if (l == 0) lds_publish(pdready, h + 1);
+        if constexpr (STORE_D) {
+            // tile h: lane l's column 16 h + (l & 15), rows 4 (l >> 4) + 16 rb + r
+            const int c = h * U + (l & 15);
+            const float* src = ring + 4 * (l >> 4) * CS + (c & (CR - 1));
+            const int col = min(c, M - 1);
+            const int row0 = b * WAVE + 4 * (l >> 4);
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = min(row0 + 16 * rb + r, N - 1);
+                    Dp[(int64_t)row * M + col] = src[(16 * rb + r) * CS];
+                }
+        }
     }
 }
 
@@ -1798,7 +1823,11 @@ SDTW_DEV void fwd_lin_roles(const DPParams& P, const Smem& sm, int p, int g, int
         return;
     }
     if (W == 1 && w >= 4) {
-        if (w == 6 && lin && g < P.nb) lin_exp_wave(P, sm, 0);
+        // (D stores here where the producer leaves them out: K == KX, see below)
+        if (w == 6 && lin && g < P.nb) {
+            if (P.D_out && P.K == KXOf<Cost>::value) lin_exp_wave<true>(P, sm, p, g, 0);
+            else lin_exp_wave<false>(P, sm, p, g, 0);
+        }
         return;
     }
     const int conv0 = W == 1 ? 3 : 6;
@@ -1811,8 +1840,10 @@ SDTW_DEV void fwd_lin_roles(const DPParams& P, const Smem& sm, int p, int g, int
     const int wb = w >= W ? w - W : w;
     if (g * W + wb >= P.nb) return;
     if (w >= W) {
+        // (W = 1, linear domain: the exponential wave stores D, so the producer does not)
         if (P.K != KXOf<Cost>::value) producer_wave<Cost, false>(P, sm, p, g * W + wb, wb);
-        else if (P.D_out) producer_wave<Cost, false, false, true, true>(P, sm, p, g * W + wb, wb);
+        else if (P.D_out && !(lin && W == 1)) producer_wave<Cost, false, false, true, true>(P, sm, p, g * W + wb, wb);
+        else if (P.D_out) producer_wave<Cost, false, false, false, true, true>(P, sm, p, g * W + wb, wb);
         else producer_wave<Cost, false, false, false, true>(P, sm, p, g * W + wb, wb);
         return;
     }
