@@ -134,21 +134,24 @@ class _no_gc:
 
 
 def time_kernel(fn, launches, warmup=2):
+    """ms per engine launch: one pair of HIP events around `launches` back-to-back launches
+    on the engine's stream (an event pair around every launch would add its own marker
+    packets, about 10 us each, between the kernels)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(launches)]
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
     with _no_gc():
-        for a, b in evs:
-            a.record(st)
+        a.record(st)
+        for _ in range(launches):
             fn()
-            b.record(st)
+        b.record(st)
         torch.cuda.synchronize()
-    return statistics.mean(a.elapsed_time(b) for a, b in evs)
+    return a.elapsed_time(b) / launches
 
 
 def time_steps(step, steps, warmup):
