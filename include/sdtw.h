@@ -200,7 +200,9 @@ int sdtw_fwd_f32_noalloc(const float *D, float *R, float *out, int64_t B, int64_
 size_t sdtw_fwd_f32_noalloc_scratch_limit(void);
 
 /* Soft-DTW backward: G[b,i,j] = gout[b] * E[b,i,j], E = d out[b] / d D[b,i,j].
- * gout may be NULL (treated as 1, i.e. G = E, what launcher.py returns).
+ * gout may be NULL (treated as 1, i.e. G = E, what launcher.py returns).  Its workspace
+ * (sdtw_workspace_bytes(SDTW_OP_BWD, ...)) depends on the device's compute-unit count: it
+ * holds one cross-workgroup row per band where the batch's one-band workgroups all fit.
  * Replaces softdtw_cuda/cuda/launcher.py:226-300 (softdtw_backward_cuda_log) together
  * with the `g * E` of autograd.py:46-47, with the numerics of launcher.py:327-353. */
 int sdtw_bwd_f32(const float *D, const float *R, const float *gout, float *G, int64_t B,

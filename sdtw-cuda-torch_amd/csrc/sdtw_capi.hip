@@ -210,6 +210,11 @@ std::atomic<int> g_numerics{SDTW_NUMERICS_MIXED};
 // forward: fp64-accurate exp / log unless FAST; backward: only in EXACT
 bool exact_forward() { return g_numerics.load(std::memory_order_relaxed) != SDTW_NUMERICS_FAST; }
 bool exact_backward() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_EXACT; }
+// The D-reading backward takes one band per workgroup, with a weight wave per band, where the
+// batch's one-band workgroups all fit at once (the weights need hardware exp2: mixed or fast
+// arithmetic).  Its workspace is sized for that geometry whatever the arithmetic.
+bool bwd_one_band(int64_t B, int64_t N) { return B * ((N + 63) / 64) <= cu_count(); }
+int bwd_wmax(int64_t B, int64_t N) { return bwd_one_band(B, N) ? 1 : 4; }
 // the fused forwards' scaled linear-domain recursion: mixed arithmetic only (exact keeps the
 // log-domain form, whose R carries the CPU path's fp32 bits)
 bool lin_forward() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_MIXED; }
@@ -335,8 +340,9 @@ size_t sdtw_workspace_bytes(int op, int64_t B, int64_t N, int64_t M, int64_t K) 
         case SDTW_OP_SQEUCLID_BWD:
             return ws_norms(B, N, M) + ws_dist_bwd(B, N, M, K);
         case SDTW_OP_FWD:
-        case SDTW_OP_BWD:
             return ws_dp(B, N, M);
+        case SDTW_OP_BWD:
+            return ws_dp(B, N, M, bwd_wmax(B, N));
         case SDTW_OP_FUSED_FWD:
             return ws_norms(B, N, M) + ws_dp(B, N, M, fused_ws_wmax(B, N, M, K, false));
         case SDTW_OP_FUSED_BWD:
@@ -454,10 +460,13 @@ int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, in
     if (B == 0) return SDTW_OK;
     if (!D || !R || !G) return SDTW_ERR_INVALID_VALUE;
     Carver c{static_cast<char*>(ws), ws_bytes};
-    const DPScratch d = carve_dp(c, B, N, M);
+    const bool ww = !exact_backward() && bwd_one_band(B, N);
+    const int wmax = ww ? 1 : 4;
+    const DPScratch d = carve_dp(c, B, N, M, wmax);
     if (!c.ok) return SDTW_ERR_WORKSPACE;
     DPParams p{};
-    fill_dp(p, d, B, N, M, 0, gamma, bandwidth);
+    fill_dp(p, d, B, N, M, 0, gamma, bandwidth, wmax);
+    p.ww = ww;
     p.D = D;
     p.R = const_cast<float*>(R);
     p.gout = gout;

@@ -661,6 +661,9 @@ struct Smem {
     SDTW_DEV unsigned* lin_red() const { return reinterpret_cast<unsigned*>(base) + 60; }
     // groups whose cost exponentials the exponential wave has staged (W = 1; int 63)
     SDTW_DEV int* lin_pdready() const { return reinterpret_cast<int*>(base) + 63; }
+    // backward with weight waves: groups whose weights weight wave k has staged (ints 56,
+    // 57, which the backward does not otherwise use)
+    SDTW_DEV int* bwd_wready() const { return reinterpret_cast<int*>(base) + 56; }
     SDTW_DEV double* tables() const { return tab; }
     SDTW_DEV unsigned char* ring() const { return base + 256; }
     SDTW_DEV float* cost_ring(int w) const {
@@ -1069,6 +1072,11 @@ SDTW_HD size_t ring_bytes_fwd(int W) { return ((size_t)(W + 1) * RS + kStageFwd)
 // (backward: then the workgroup's staging block of kStageBwd bytes, see bwd_band)
 constexpr int kStageBwd = 12 * WAVE + 16 * U + 16 * U;
 SDTW_HD size_t ring_bytes_bwd(int W) { return (size_t)(W + 1) * RS * sizeof(float4) + kStageBwd; }
+// Backward with a weight wave (W = 1): after the handoff rings and the staging block, the
+// weight stage, kWBufs groups of U steps x 64 lanes of float4 (a, b, c, unused), so that
+// each lane's per-step read and write is one 16-byte access, conflict-free.
+constexpr int kWBufs = 3;
+constexpr size_t kWStageBytes = (size_t)kWBufs * U * WAVE * sizeof(float4);
 
 // Forward in the scaled linear domain (fwd_band_lin): LDS after the staging block.  The
 // handoff rings keep their p values in the slots of the log-domain rings; their exponents
@@ -1085,6 +1093,7 @@ SDTW_HD size_t lin_extra_bytes(int W) {
     return (size_t)(W + 1) * RS * 4 + (size_t)W * 2 * kLinBuf * 12 + (W == 1 ? (size_t)kPdBufs * kLinBuf * 12 : 0);
 }
 SDTW_DEV int* lin_ering(const Smem& sm) { return reinterpret_cast<int*>(sm.ring() + ring_bytes_fwd(sm.W)); }
+SDTW_DEV float4* bwd_wstage(const Smem& sm) { return reinterpret_cast<float4*>(sm.ring() + ring_bytes_bwd(sm.W)); }
 SDTW_DEV double* lin_stage_p(const Smem& sm, int w, int k) {
     return reinterpret_cast<double*>(lin_ering(sm) + (sm.W + 1) * RS) + (w * 2 + k) * kLinBuf;
 }
@@ -1937,8 +1946,13 @@ __global__ void __launch_bounds__(8 * WAVE) fwd_lin_kernel(DPParams P) {
 // (launcher.py:330-338); row N-1 takes its down/diag from that padding directly.  Each
 // visited cell maps R = +inf to -inf first (launcher.py:343-344).
 // ---------------------------------------------------------------------------------------
-template <class Cost, bool BAND, bool EXACT>
+// WW: the weight waves of the band (bwd_weight_wave) stage each cell's three weights, and
+// this wave's step is the E recurrence on them (the same operations as bwd_cell_hw's, so the
+// same bits); the bands hand over E alone (the R and D slots of the handoff entries are not
+// written).
+template <class Cost, bool BAND, bool EXACT, bool WW = false>
 SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int g, int w) {
+    static_assert(!WW || !EXACT, "weight wave: hardware exp2 backward only");
     const int l = threadIdx.x & (WAVE - 1);
     const int W = P.W, G = P.G, nb = P.nb, N = P.N, M = P.M, S = P.S;
     const int b = g * W + w;
@@ -1981,6 +1995,9 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     float4* stage_glb = reinterpret_cast<float4*>(stage + 12 * WAVE + 16 * U);
 
     const float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
+    const float4* wst = bwd_wstage(sm) + l;  // WW: this lane's entries of the weight stage
+    const int* wready = sm.bwd_wready();  // [group parity]
+    int known_w0 = 0, known_w1 = 0;
 
     int known_in = 0, known_free = 0;
     float rE = 0.0f, rR = NINF, rD = 0.0f;  // right neighbour
@@ -2055,10 +2072,12 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         return;
     }
     cost.preload(tile_col(2 * TC));
+    if constexpr (!WW) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        r_nxt[u] = Rt[(int64_t)fstep(u) * WAVE];
-        d_nxt[u] = crow[ring_col(u)];
+        for (int u = 0; u < U; ++u) {
+            r_nxt[u] = Rt[(int64_t)fstep(u) * WAVE];
+            d_nxt[u] = crow[ring_col(u)];
+        }
     }
 
     // One group: 16 reverse steps from q0.  INTERIOR: every lane is inside the table for all
@@ -2072,10 +2091,12 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
     // provider the extra body costs more registers than it saves.
     auto group = [&](int q0, auto interior_tag) -> bool {
         constexpr bool INTERIOR = decltype(interior_tag)::value;
+        if constexpr (!WW) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            r_cur[u] = r_nxt[u];
-            d_cur[u] = d_nxt[u];
+            for (int u = 0; u < U; ++u) {
+                r_cur[u] = r_nxt[u];
+                d_cur[u] = d_nxt[u];
+            }
         }
         // the counters this group start checks, loaded together (one LDS round trip; each
         // wait below then polls only if its cached count falls short)
@@ -2084,10 +2105,19 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             const int v_free = lds_load(sm.cons() + w);
             if constexpr (std::is_same<Cost, CostRing>::value)
                 cost.known = max(cost.known, __builtin_amdgcn_readfirstlane(lds_load(cost.ready)));
+            if constexpr (WW) {
+                known_w0 = max(known_w0, __builtin_amdgcn_readfirstlane(lds_load(wready)));
+                known_w1 = max(known_w1, __builtin_amdgcn_readfirstlane(lds_load(wready + 1)));
+            }
             known_in = max(known_in, __builtin_amdgcn_readfirstlane(v_in));
             known_free = max(known_free, __builtin_amdgcn_readfirstlane(v_free));
         }
+        const int gi = q0 / U;
+        if (WW && !((gi & 1) ? wait_at_least(wready + 1, gi / 2 + 1, known_w1, P.err, P.spin_limit)
+                             : wait_at_least(wready, gi / 2 + 1, known_w0, P.err, P.spin_limit)))
+            return false;
         if (!cost.begin(cring, tile_col(q0 + 2 * TC)) || !fetch_lds(q0, dn_cur)) return false;
+        const float4* wbuf = wst + (gi % kWBufs) * (U * WAVE);
         const int n0 = q0 + U;
         if (out_lds) {  // as in the forward: sequence numbers up to q0 + U - 64 this group
             const int need_free = q0 + U - WAVE + 1 - RS;
@@ -2104,6 +2134,24 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         for (int u = 0; u < U; ++u) {
             const int q = q0 + u;
             const int j = (M - 1) - q + (WAVE - 1 - l);
+            if constexpr (WW) {
+                const float4 wt = wbuf[u * WAVE];  // (down, right, diag) weights
+                float dE = __int_as_float(dpp_shl1(__float_as_int(dn_cur[u].x), __float_as_int(pE)));
+                if (!INTERIOR && last_row) dE = (j == M) ? 1.0f : 0.0f;
+                const bool act = INTERIOR || (row_ok && (unsigned)j < (unsigned)M);
+                const float cand = __fmaf_rn(gE, wt.z, __fmaf_rn(rE, wt.y, __fmul_rn(dE, wt.x)));
+                bool keep = true;
+                if (BAND && !INTERIOR) keep = !out_of_band(bw, i, j);
+                const float e = keep ? cand : 0.0f;
+                crow[j & (CR - 1)] = __fmul_rn(gsc, e);
+                const float mE = act ? e : 0.0f;
+                rE = mE;
+                gE = dE;
+                pE = mE;
+                dst[4 * u] = mE;
+                cost.step(u, tile_col(q0 + 2 * TC), tile_col(q0 + 3 * TC));
+                continue;
+            }
             float dE = __int_as_float(dpp_shl1(__float_as_int(dn_cur[u].x), __float_as_int(pE)));
             float dR = __int_as_float(dpp_shl1(__float_as_int(dn_cur[u].y), __float_as_int(pR)));
             float dD = __int_as_float(dpp_shl1(__float_as_int(dn_cur[u].z), __float_as_int(pD)));
@@ -2164,6 +2212,133 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
         if (!group(q0, std::false_type{})) return give_up_bwd(P, p, b);
 }
 
+// Weight waves of band b (the backward with costs read from D, hardware exp2, one band per
+// workgroup).  The cell's weights (launcher.py:347-351)
+//   a = exp((R(i+1,j) - R(i,j) - D(i+1,j)) / gamma)    (down)
+//   b = exp((R(i,j+1) - R(i,j) - D(i,j+1)) / gamma)    (right)
+//   c = exp((R(i+1,j+1) - R(i,j) - D(i+1,j+1)) / gamma) (diagonal)
+// depend only on the forward's R and on D, both in memory before the launch, including the
+// row below the band (the band below's first row, which lane 63 reads from its R table and
+// from D).  Two waves form them, wave k for the groups h = k mod 2, with bwd_cell_hw's
+// operations on the values the compute wave would use (the same masking of inactive cells,
+// +inf mapped to -inf, the padding row and corner below the table), ahead of the compute
+// wave, into a three-buffer LDS stage (group h in buffer h % kWBufs; wave k counts its
+// groups in bwd_wready()[k]).  A wave's state at the start of group h (its cell and the cell
+// below one step earlier, whose weights the other wave formed) is read from memory again.
+// It reads a group's costs from the band's cost ring once the producer has published the
+// tile after them (the compute wave's own rule), and writes buffer h % kWBufs once the
+// compute wave has finished group h - kWBufs.  Its waits are bounded; on expiry it stops,
+// and the compute wave's bounded wait for its count then gives up for the band.
+SDTW_DEV void bwd_weight_wave(const DPParams& P, const Smem& sm, int p, int b, int k) {
+    const int l = threadIdx.x & (WAVE - 1);
+    const int nb = P.nb, N = P.N, M = P.M, S = P.S;
+    const int i = b * WAVE + l;
+    const bool row_ok = i < N;
+    const bool last_row = (i == N - 1);
+    const float c2 = (float)(P.inv_gamma * 1.4426950408889634074);  // log2(e) / gamma
+    const float NINF = -finf();
+    const int lb = nb - 1, ll = (N - 1) - lb * WAVE;
+    const float corner_R = P.R[(((int64_t)p * nb + lb) * S + (M - 1 + ll)) * WAVE + ll];
+    const float* crow = sm.cost_ring(0) + l * CS;
+    const float* Rt = P.R + ((int64_t)p * nb + b) * S * WAVE + l;
+    const float* Dp = P.D + (int64_t)p * N * M;
+    // the row below: lane 0 of band b + 1 (its entry of forward step j is column j) and
+    // row (b + 1) * 64 of D; none below the last band (the padding row: R -inf, D 0)
+    const bool below = b + 1 < nb;
+    const float* Rb = P.R + ((int64_t)p * nb + (below ? b + 1 : b)) * S * WAVE;
+    const float* Db = Dp + (int64_t)(below ? b + 1 : b) * WAVE * M;
+    // the cell below this lane's, (i + 1, j): band and lane of row i + 1 (clamped)
+    const int rdn = min(i + 1, N - 1), bdn = rdn / WAVE, ldn = rdn - bdn * WAVE;
+    const float* Rdn = P.R + ((int64_t)p * nb + bdn) * S * WAVE + ldn;
+    float4* stage = bwd_wstage(sm) + l;
+    int* wready = sm.bwd_wready() + k;
+    const int* ready = sm.ready();
+    const int* done = sm.done();
+    int known_ready = 0, known_done = 0;
+    const int groups = S / U;
+    auto fstep = [&](int q) { return max(M + 62 - q, 0); };
+    // for the group at q0: this lane's R; (lanes u < U) the row below at lane 63's column of
+    // step q0 + u, M - 1 - q0 - u; and the R and D of this lane's cell and of the cell below
+    // it at step q0 - 1 (column jp), from which the group's starting state is formed
+    float r_nxt[U];
+    float bR_nxt = NINF, bD_nxt = 0.0f, oR_nxt = NINF, oD_nxt = 0.0f, uR_nxt = NINF, uD_nxt = 0.0f;
+    auto fetch = [&](int q0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) r_nxt[u] = Rt[(int64_t)fstep(q0 + u) * WAVE];
+        const int jb = M - 1 - q0 - l;
+        const bool ok = below && l < U && jb >= 0;
+        const float rb = Rb[(int64_t)max(jb, 0) * WAVE];
+        const float db = Db[max(jb, 0)];
+        bR_nxt = ok ? (__builtin_isinf(rb) ? NINF : rb) : NINF;
+        bD_nxt = ok ? db : 0.0f;
+        const int jp = min(max((M - 1) - (q0 - 1) + (WAVE - 1 - l), 0), M - 1);
+        oR_nxt = Rt[(int64_t)min(fstep(q0 - 1), S - 1) * WAVE];
+        oD_nxt = Dp[(int64_t)min(i, N - 1) * M + jp];
+        uR_nxt = Rdn[(int64_t)min(jp + ldn, S - 1) * WAVE];
+        uD_nxt = Dp[(int64_t)rdn * M + jp];
+    };
+    float rR = NINF, rD = 0.0f;                       // right neighbour
+    float gR = last_row ? corner_R : NINF, gD = 0.0f;  // diagonal neighbour
+    float pR = NINF, pD = 0.0f;                       // this lane's cell one step ago
+    fetch(k * U);
+    for (int h = k; h < groups; h += 2) {
+        const int q0 = h * U;
+        float r_cur[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) r_cur[u] = r_nxt[u];
+        const float bR = bR_nxt, bD = bD_nxt;
+        if (h > 0) {  // the state after step q0 - 1
+            const int jp = (M - 1) - (q0 - 1) + (WAVE - 1 - l);
+            const bool act_p = row_ok && (unsigned)jp < (unsigned)M;
+            pR = act_p ? (__builtin_isinf(oR_nxt) ? NINF : oR_nxt) : NINF;
+            pD = act_p ? oD_nxt : 0.0f;
+            rR = pR;
+            rD = pD;
+            const bool act_dn = (i + 1 < N) && (unsigned)jp < (unsigned)M;
+            gR = act_dn ? (__builtin_isinf(uR_nxt) ? NINF : uR_nxt) : NINF;
+            gD = act_dn ? uD_nxt : 0.0f;
+            if (last_row) {
+                gR = (jp == M) ? corner_R : NINF;
+                gD = 0.0f;
+            }
+        }
+        if (h + 2 < groups) fetch(q0 + 2 * U);
+        if (!wait_at_least(ready, h + 2, known_ready, P.err, P.spin_limit)) return;
+        if (h >= kWBufs && !wait_at_least(done, h - kWBufs + 1, known_done, P.err, P.spin_limit)) return;
+        float4* buf = stage + (h % kWBufs) * (U * WAVE);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = q0 + u;
+            const int j = (M - 1) - q + (WAVE - 1 - l);
+            const float sR = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bR), u));
+            const float sD = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bD), u));
+            float dR = __int_as_float(dpp_shl1(__float_as_int(sR), __float_as_int(pR)));
+            float dD = __int_as_float(dpp_shl1(__float_as_int(sD), __float_as_int(pD)));
+            if (last_row) {  // the padded row below the table
+                dR = (j == M) ? corner_R : NINF;
+                dD = 0.0f;
+            }
+            const bool act = row_ok && (unsigned)j < (unsigned)M;
+            float rij = r_cur[u];
+            rij = __builtin_isinf(rij) ? NINF : rij;
+            const float d = crow[j & (CR - 1)];
+            const float wa = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(dR, rij), dD), c2));
+            const float wb = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(rR, rij), rD), c2));
+            const float wg = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(gR, rij), gD), c2));
+            buf[u * WAVE] = make_float4(wa, wb, wg, 0.0f);
+            const float mR = act ? rij : NINF;
+            const float mD = act ? d : 0.0f;
+            rR = mR;
+            rD = mD;
+            gR = dR;
+            gD = dD;
+            pR = mR;
+            pD = mD;
+        }
+        if (l == 0) lds_publish(wready, h / 2 + 1);
+    }
+}
+
 // GW > 0: gradient mode for workgroups of up to GW bands.  GW = 2: waves compute 0 .. W-1,
 // producers W .. 2W-1, dL/dy waves 2W .. 3W-1, dL/dx waves 3W .. 4W-1, helper 4W (under
 // round-robin placement with W = 2 the dL/dy waves share the compute waves' SIMDs and the
@@ -2178,7 +2353,12 @@ bwd_kernel(DPParams P) {
     static_assert(GW == 0 || KXOf<Cost>::value > 0, "gradient mode needs matrix-core cost tiles");
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ __align__(16) double tab[kTabBytesBwd / 8];
-    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W), kTabBytesBwd, tab};
+    // with weight waves (P.ww: costs from D, hardware exp2, W = 1; waves compute 0,
+    // producer 1, helper 2, weights 3 and 5, 4 idle, so that each weight wave shares its
+    // SIMD with a light wave) their stage follows the handoff rings
+    constexpr bool WW_OK = std::is_same<Cost, CostD>::value && !EXACT && GW == 0;
+    const bool ww = WW_OK && P.ww;
+    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W) + (ww ? kWStageBytes : 0), kTabBytesBwd, tab};
     // wave-uniform values are moved to scalar registers so that the branches on band,
     // group and pair compile to scalar branches, not exec-masked regions
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -2186,6 +2366,7 @@ bwd_kernel(DPParams P) {
     if (threadIdx.x < 2 * (P.W + 1)) sm.prod()[threadIdx.x] = 0;
     if (threadIdx.x < 16) sm.ready()[threadIdx.x] = 0;
     if (threadIdx.x < 8) sm.gdone()[threadIdx.x] = 0;
+    if (threadIdx.x < 2) sm.bwd_wready()[threadIdx.x] = 0;
     sm.load_tables();
     __syncthreads();
     const int t = __builtin_amdgcn_readfirstlane(*sm.ticket());
@@ -2214,6 +2395,20 @@ bwd_kernel(DPParams P) {
             bwd_band<CostRing, BAND, EXACT>(P, cost, sm, p, g, w);
         }
     } else if constexpr (Produced<Cost, true>::value) {
+        if constexpr (WW_OK) {
+            if (ww) {  // one band per workgroup (g is the band)
+                if (w == 3 || w == 5) {
+                    bwd_weight_wave(P, sm, p, g, w == 3 ? 0 : 1);
+                } else if (w == 1) {
+                    producer_wave<Cost, true>(P, sm, p, g, 0);
+                } else if (w == 0) {
+                    CostRing cost;
+                    cost.bind(sm, 0, P);
+                    bwd_band<CostRing, BAND, false, true>(P, cost, sm, p, g, 0);
+                }
+                return;
+            }
+        }
         const int wb = w >= P.W ? w - P.W : w;
         if (g * P.W + wb >= P.nb) return;
         if (w >= P.W) {
@@ -2238,7 +2433,8 @@ bwd_kernel(DPParams P) {
 hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st);
 
 inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
-    const size_t ring = bwd ? ring_bytes_bwd(P.W) : ring_bytes_fwd(P.W) + (P.lin ? lin_extra_bytes(P.W) : 0);
+    const size_t ring = bwd ? ring_bytes_bwd(P.W) + (P.ww ? kWStageBytes : 0)
+                            : ring_bytes_fwd(P.W) + (P.lin ? lin_extra_bytes(P.W) : 0);
     return 256 + ring + (size_t)P.W * WAVE * CS * sizeof(float);  // the tables are static
 }
 
@@ -2258,6 +2454,7 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipSt
     // (a launch that can take the linear domain: a converter wave per band, fwd_lin_roles)
     const int waves = grad ? (P.W <= 2 ? 4 : 3) * P.W + 1
                       : !bwd && P.lin ? (P.W == 1 ? 7 : 8)
+                      : bwd && P.ww ? 6
                       : (produced ? 2 * P.W + 1 : P.W + (P.G > 1 ? 1 : 0));
     hipLaunchKernelGGL(kernel, dim3(P.B * P.G), dim3(waves * WAVE), lds, st, P);
     return hipGetLastError();
@@ -2266,8 +2463,11 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipSt
 template <class Cost, bool BWD, bool EXACT>
 hipError_t launch_cost(const DPParams& P, hipStream_t st) {
     if constexpr (BWD) {
-        if (P.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT>, P, true, Produced<Cost, true>::value, st);
-        return launch_dp(bwd_kernel<Cost, false, EXACT>, P, true, Produced<Cost, true>::value, st);
+        // the weight wave only where the kernel has it (costs from D, hardware exp2, W = 1)
+        DPParams Q = P;
+        if (!std::is_same<Cost, CostD>::value || EXACT || P.W != 1) Q.ww = 0;
+        if (Q.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT>, Q, true, Produced<Cost, true>::value, st);
+        return launch_dp(bwd_kernel<Cost, false, EXACT>, Q, true, Produced<Cost, true>::value, st);
     } else {
         // the linear domain only where the kernel can take it
         DPParams Q = P;

@@ -41,6 +41,9 @@ struct DPParams {
     int lin;            // forward under mixed arithmetic, matrix-core costs, no band, W <= 2:
                         // pairs whose costs allow it run the scaled linear-domain recursion
                         // (fwd_band_lin)
+    int ww;             // backward with costs read from D, hardware exp2 (mixed or fast
+                        // arithmetic), W == 1: a weight wave per band forms each cell's three
+                        // weights ahead of the compute wave (bwd_weight_wave)
     int nb, W, G;       // 64-row bands per pair, waves per workgroup, workgroups per pair
     int S;              // steps per band in the R table (dp_band_steps(M))
     double gamma, inv_gamma, bw;

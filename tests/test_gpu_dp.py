@@ -232,6 +232,38 @@ def test_fused_matches_unfused_kernels(mode):
             torch.testing.assert_close(o2.cpu(), out_o, rtol=FWD_RTOL, atol=0)
 
 
+@pytest.mark.parametrize("mode", ["mixed", "fast"])
+@pytest.mark.parametrize("B,N,M,gamma,bw", [
+    (4, 512, 512, 1.0, -1.0),    # full bands, the row below read from the next band's R and D
+    (3, 150, 120, 0.7, 30.0),    # Sakoe-Chiba band, a partial last band
+    (2, 100, 77, 0.1, -1.0),     # sharp soft-min, the corner inside a partial band
+    (3, 70, 10, 1.0, -1.0),      # fewer columns than a group
+])
+def test_weight_wave_backward_matches_classic(mode, B, N, M, gamma, bw):
+    # The D-reading backward under hardware exp2 takes one band per workgroup with a weight
+    # wave where the batch's one-band workgroups all fit on the GPU, else the classic
+    # geometry (4 bands per workgroup, the weights in the compute wave).  Pairs are
+    # independent, so the same pairs inside a batch too large for one-band workgroups give
+    # the classic result: G must be identical to the bit, with an upstream gradient too.
+    nb = (N + 63) // 64
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    Bbig = cus // nb + 1
+    assert B * nb <= cus < Bbig * nb
+    say(f"[weight wave] mode={mode} B={B} (classic batch {Bbig}) N={N} M={M} gamma={gamma} bw={bw}")
+    x, y = randn_pair(Bbig, N, M, 6, seed=N + M)
+    with numerics(mode):
+        D = _engine.sqeuclid_fwd(x.cuda(), y.cuda())
+        _, R = _engine.dtw_fwd(D, gamma, bw)
+        g = torch.linspace(0.5, 2.0, Bbig, device=D.device)
+        Gbig = _engine.dtw_bwd(D, R, gamma, bw, gout=g)
+        Ds = D[:B].contiguous()
+        S = (M + 63 + 15) // 16 * 16  # steps per band of the R table (pairs are contiguous)
+        Rs = R[:B * nb * S * 64].contiguous()
+        Gs = _engine.dtw_bwd(Ds, Rs, gamma, bw, gout=g[:B].contiguous())
+    assert torch.isfinite(Gs).all()
+    assert torch.equal(Gs, Gbig[:B])
+
+
 @pytest.mark.parametrize("B,N,M,K,gamma,scale", [
     (32, 512, 512, 64, 1.0, None),   # the headline shape: one band per workgroup
     (64, 512, 128, 16, 0.5, None),   # 512 bands: two per workgroup (LDS and global handover)
