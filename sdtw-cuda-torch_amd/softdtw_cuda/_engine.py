@@ -8,6 +8,7 @@ missing or no GPU is present, they raise.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 
@@ -90,6 +91,9 @@ def library_path() -> str:
 def load():
     """Load libsdtw_hip.so (once).  Raises RuntimeError if it has not been built."""
     global _lib
+    lib = _lib
+    if lib is not None:  # loaded: no lock needed to read it
+        return lib
     with _lock:
         if _lib is not None:
             return _lib
@@ -170,6 +174,7 @@ def require_gpu(t: torch.Tensor, what: str, dtype=torch.float32):
         raise RuntimeError(f"softdtw_cuda: {what} expects contiguous {dtype}, got {t.dtype}")
 
 
+@functools.lru_cache(maxsize=256)
 def table_elems(B, N, M) -> int:
     """Floats in the engine's R table for B pairs of N x M cells."""
     return int(load().sdtw_table_elems(B, N, M))
@@ -246,14 +251,29 @@ def _debug_check(op, ws, nws, B, N, M, K, what):
         _check(load().sdtw_debug_status(op, _ptr(ws), nws, B, N, M, K), what + " (debug status)")
 
 
+_ws_sizes = {}
+
+
+def _device_index(device) -> int:
+    d = torch.device(device)
+    return d.index if d.index is not None else torch.cuda.current_device()
+
+
 def _workspace(op, B, N, M, K, device):
-    # the size can depend on the device (the fused recursions' workgroup geometry follows its
-    # CU count), so it is queried with that device current
-    with torch.cuda.device(device):
-        n = int(load().sdtw_workspace_bytes(op, B, N, M, K))
+    """The workspace of one engine call.  Its size depends on the shape, the device (the
+    recursions' workgroup geometry follows its CU count: queried with that device current),
+    the arithmetic and the deterministic setting, and is cached under all of them; the buffer
+    is allocated per call."""
+    idx = _device_index(device)
+    key = (op, B, N, M, K, idx, int(load().sdtw_get_numerics()), _deterministic)
+    n = _ws_sizes.get(key)
+    if n is None:
+        with torch.cuda.device(idx):
+            n = int(load().sdtw_workspace_bytes(op, B, N, M, K))
+        _ws_sizes[key] = n
     if n == 0:
         return None, 0
-    return torch.empty(n, dtype=torch.uint8, device=device), n
+    return torch.empty(n, dtype=torch.uint8, device=torch.device("cuda", idx)), n
 
 
 def sqeuclid_fwd(x: torch.Tensor, y: torch.Tensor, mode: int = DIST_EXACT) -> torch.Tensor:
@@ -375,12 +395,21 @@ def fused_costs_on_matrix_cores(N: int, M: int, K: int) -> bool:
     return K <= 64 and K * N * M >= 400
 
 
+_bands_cache = {}
+
+
 def fused_bands_per_workgroup(B: int, N: int, M: int, K: int, device) -> int:
     """The fused forward recursions' bands per workgroup for an unbanded call at this shape
     on `device` under the current arithmetic (the library's own choice,
-    sdtw_fused_bands_per_workgroup): 1, 2 or 4."""
-    with torch.cuda.device(device):
-        return int(load().sdtw_fused_bands_per_workgroup(B, N, M, K))
+    sdtw_fused_bands_per_workgroup): 1, 2 or 4.  Cached per shape, device and arithmetic."""
+    idx = _device_index(device)
+    key = (B, N, M, K, idx, int(load().sdtw_get_numerics()))
+    w = _bands_cache.get(key)
+    if w is None:
+        with torch.cuda.device(idx):
+            w = int(load().sdtw_fused_bands_per_workgroup(B, N, M, K))
+        _bands_cache[key] = w
+    return w
 
 
 def one_launch_unfused_forward(B: int, N: int, M: int, K: int, device) -> bool:
@@ -395,6 +424,11 @@ def one_launch_unfused_forward(B: int, N: int, M: int, K: int, device) -> bool:
     return fused_bands_per_workgroup(B, N, M, K, device) <= 2
 
 
+@functools.lru_cache(maxsize=256)
+def _dist_record_bytes(B, N, M) -> int:
+    return int(load().sdtw_dist_record_bytes(B, N, M))
+
+
 def fused_fwd_d(x, y, gamma: float, bandwidth: float):
     """Unfused mode's forward in one launch: (out, R, D, record) with D the (B,N,M) cost
     tensor and record its distance record for sqeuclid_bwd (uint8 device buffer: per-pair
@@ -407,8 +441,7 @@ def fused_fwd_d(x, y, gamma: float, bandwidth: float):
     D = torch.empty((B, N, M), dtype=torch.float32, device=x.device)
     R = torch.empty((table_elems(B, N, M),), dtype=torch.float32, device=x.device)
     out = torch.empty((B,), dtype=torch.float32, device=x.device)
-    record = torch.empty((int(load().sdtw_dist_record_bytes(B, N, M)),), dtype=torch.uint8,
-                         device=x.device)
+    record = torch.empty((_dist_record_bytes(B, N, M),), dtype=torch.uint8, device=x.device)
     ws, nws = _workspace(OP_FUSED_FWD, B, N, M, K, x.device)
     with torch.cuda.device(x.device):
         rc = load().sdtw_fused_fwd_d_f32(_ptr(x), _ptr(y), _ptr(D), _ptr(record), _ptr(R),
