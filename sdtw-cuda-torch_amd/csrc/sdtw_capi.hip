@@ -210,9 +210,8 @@ std::atomic<int> g_numerics{SDTW_NUMERICS_MIXED};
 // forward: fp64-accurate exp / log unless FAST; backward: only in EXACT
 bool exact_forward() { return g_numerics.load(std::memory_order_relaxed) != SDTW_NUMERICS_FAST; }
 bool exact_backward() { return g_numerics.load(std::memory_order_relaxed) == SDTW_NUMERICS_EXACT; }
-// The D-reading backward takes one band per workgroup, with a weight wave per band, where the
-// batch's one-band workgroups all fit at once (the weights need hardware exp2: mixed or fast
-// arithmetic).  Its workspace is sized for that geometry whatever the arithmetic.
+// The D-reading backward takes one band per workgroup, with weight waves per band, where the
+// batch's one-band workgroups all fit at once.  Its workspace is sized for that geometry.
 bool bwd_one_band(int64_t B, int64_t N) { return B * ((N + 63) / 64) <= cu_count(); }
 int bwd_wmax(int64_t B, int64_t N) { return bwd_one_band(B, N) ? 1 : 4; }
 // the fused forwards' scaled linear-domain recursion: mixed arithmetic only (exact keeps the
@@ -460,7 +459,7 @@ int sdtw_bwd_f32(const float* D, const float* R, const float* gout, float* G, in
     if (B == 0) return SDTW_OK;
     if (!D || !R || !G) return SDTW_ERR_INVALID_VALUE;
     Carver c{static_cast<char*>(ws), ws_bytes};
-    const bool ww = !exact_backward() && bwd_one_band(B, N);
+    const bool ww = bwd_one_band(B, N);
     const int wmax = ww ? 1 : 4;
     const DPScratch d = carve_dp(c, B, N, M, wmax);
     if (!c.ok) return SDTW_ERR_WORKSPACE;

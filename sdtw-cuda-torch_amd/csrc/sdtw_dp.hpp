@@ -1072,11 +1072,12 @@ SDTW_HD size_t ring_bytes_fwd(int W) { return ((size_t)(W + 1) * RS + kStageFwd)
 // (backward: then the workgroup's staging block of kStageBwd bytes, see bwd_band)
 constexpr int kStageBwd = 12 * WAVE + 16 * U + 16 * U;
 SDTW_HD size_t ring_bytes_bwd(int W) { return (size_t)(W + 1) * RS * sizeof(float4) + kStageBwd; }
-// Backward with a weight wave (W = 1): after the handoff rings and the staging block, the
+// Backward with weight waves (W = 1): after the handoff rings and the staging block, the
 // weight stage, kWBufs groups of U steps x 64 lanes of float4 (a, b, c, unused), so that
-// each lane's per-step read and write is one 16-byte access, conflict-free.
+// each lane's per-step read and write is one 16-byte access, conflict-free.  Under exact
+// arithmetic the weights are doubles: two such planes, double2 (a, b) then (c, NaN flag).
 constexpr int kWBufs = 3;
-constexpr size_t kWStageBytes = (size_t)kWBufs * U * WAVE * sizeof(float4);
+constexpr size_t kWStageBytes = (size_t)kWBufs * U * WAVE * sizeof(float4);  // per plane
 
 // Forward in the scaled linear domain (fwd_band_lin): LDS after the staging block.  The
 // handoff rings keep their p values in the slots of the log-domain rings; their exponents
@@ -1947,12 +1948,11 @@ __global__ void __launch_bounds__(8 * WAVE) fwd_lin_kernel(DPParams P) {
 // visited cell maps R = +inf to -inf first (launcher.py:343-344).
 // ---------------------------------------------------------------------------------------
 // WW: the weight waves of the band (bwd_weight_wave) stage each cell's three weights, and
-// this wave's step is the E recurrence on them (the same operations as bwd_cell_hw's, so the
-// same bits); the bands hand over E alone (the R and D slots of the handoff entries are not
-// written).
+// this wave's step is the E recurrence on them (the same operations as bwd_cell_hw's or
+// bwd_cell_exact's, so the same bits); the bands hand over E alone (the R and D slots of the
+// handoff entries are not written).
 template <class Cost, bool BAND, bool EXACT, bool WW = false>
 SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int g, int w) {
-    static_assert(!WW || !EXACT, "weight wave: hardware exp2 backward only");
     const int l = threadIdx.x & (WAVE - 1);
     const int W = P.W, G = P.G, nb = P.nb, N = P.N, M = P.M, S = P.S;
     const int b = g * W + w;
@@ -2118,6 +2118,9 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             return false;
         if (!cost.begin(cring, tile_col(q0 + 2 * TC)) || !fetch_lds(q0, dn_cur)) return false;
         const float4* wbuf = wst + (gi % kWBufs) * (U * WAVE);
+        // (exact: plane 0 holds (a, b), plane 1 (c, NaN flag), as double2)
+        const double2* wq0 = reinterpret_cast<const double2*>(wbuf);
+        const double2* wq1 = wq0 + kWBufs * U * WAVE;
         const int n0 = q0 + U;
         if (out_lds) {  // as in the forward: sequence numbers up to q0 + U - 64 this group
             const int need_free = q0 + U - WAVE + 1 - RS;
@@ -2135,11 +2138,20 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
             const int q = q0 + u;
             const int j = (M - 1) - q + (WAVE - 1 - l);
             if constexpr (WW) {
-                const float4 wt = wbuf[u * WAVE];  // (down, right, diag) weights
                 float dE = __int_as_float(dpp_shl1(__float_as_int(dn_cur[u].x), __float_as_int(pE)));
                 if (!INTERIOR && last_row) dE = (j == M) ? 1.0f : 0.0f;
                 const bool act = INTERIOR || (row_ok && (unsigned)j < (unsigned)M);
-                const float cand = __fmaf_rn(gE, wt.z, __fmaf_rn(rE, wt.y, __fmul_rn(dE, wt.x)));
+                float cand;
+                if constexpr (EXACT) {  // bwd_cell_exact's sum on the staged weights
+                    const double2 ab = wq0[u * WAVE], cf = wq1[u * WAVE];
+                    double acc = __dmul_rn((double)dE, ab.x);
+                    acc = __dadd_rn(acc, __dmul_rn((double)rE, ab.y));
+                    acc = __dadd_rn(acc, __dmul_rn((double)gE, cf.x));
+                    cand = (float)(cf.y != 0.0 ? __builtin_nan("") : acc);
+                } else {  // (down, right, diag) weights
+                    const float4 wt = wbuf[u * WAVE];
+                    cand = __fmaf_rn(gE, wt.z, __fmaf_rn(rE, wt.y, __fmul_rn(dE, wt.x)));
+                }
                 bool keep = true;
                 if (BAND && !INTERIOR) keep = !out_of_band(bw, i, j);
                 const float e = keep ? cand : 0.0f;
@@ -2229,6 +2241,7 @@ SDTW_DEV void bwd_band(const DPParams& P, Cost& cost, const Smem& sm, int p, int
 // tile after them (the compute wave's own rule), and writes buffer h % kWBufs once the
 // compute wave has finished group h - kWBufs.  Its waits are bounded; on expiry it stops,
 // and the compute wave's bounded wait for its count then gives up for the band.
+template <bool EXACT>
 SDTW_DEV void bwd_weight_wave(const DPParams& P, const Smem& sm, int p, int b, int k) {
     const int l = threadIdx.x & (WAVE - 1);
     const int nb = P.nb, N = P.N, M = P.M, S = P.S;
@@ -2236,6 +2249,8 @@ SDTW_DEV void bwd_weight_wave(const DPParams& P, const Smem& sm, int p, int b, i
     const bool row_ok = i < N;
     const bool last_row = (i == N - 1);
     const float c2 = (float)(P.inv_gamma * 1.4426950408889634074);  // log2(e) / gamma
+    const double inv_gamma = P.inv_gamma;
+    const double* tabE = sm.tables();  // exp table in LDS (exact)
     const float NINF = -finf();
     const int lb = nb - 1, ll = (N - 1) - lb * WAVE;
     const float corner_R = P.R[(((int64_t)p * nb + lb) * S + (M - 1 + ll)) * WAVE + ll];
@@ -2306,6 +2321,8 @@ SDTW_DEV void bwd_weight_wave(const DPParams& P, const Smem& sm, int p, int b, i
         if (!wait_at_least(ready, h + 2, known_ready, P.err, P.spin_limit)) return;
         if (h >= kWBufs && !wait_at_least(done, h - kWBufs + 1, known_done, P.err, P.spin_limit)) return;
         float4* buf = stage + (h % kWBufs) * (U * WAVE);
+        double2* q0p = reinterpret_cast<double2*>(buf);
+        double2* q1p = q0p + kWBufs * U * WAVE;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int q = q0 + u;
@@ -2322,10 +2339,22 @@ SDTW_DEV void bwd_weight_wave(const DPParams& P, const Smem& sm, int p, int b, i
             float rij = r_cur[u];
             rij = __builtin_isinf(rij) ? NINF : rij;
             const float d = crow[j & (CR - 1)];
-            const float wa = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(dR, rij), dD), c2));
-            const float wb = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(rR, rij), rD), c2));
-            const float wg = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(gR, rij), gD), c2));
-            buf[u * WAVE] = make_float4(wa, wb, wg, 0.0f);
+            if constexpr (EXACT) {  // bwd_cell_exact's weights
+                const float da = __fsub_rn(__fsub_rn(dR, rij), dD);
+                const float db = __fsub_rn(__fsub_rn(rR, rij), rD);
+                const float dc = __fsub_rn(__fsub_rn(gR, rij), gD);
+                const bool nan_in = (da != da) || (db != db) || (dc != dc);
+                const double wa = fm::exp_tab((double)da * inv_gamma, tabE);
+                const double wb = fm::exp_tab((double)db * inv_gamma, tabE);
+                const double wg = fm::exp_tab((double)dc * inv_gamma, tabE);
+                q0p[u * WAVE] = make_double2(wa, wb);
+                q1p[u * WAVE] = make_double2(wg, nan_in ? 1.0 : 0.0);
+            } else {
+                const float wa = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(dR, rij), dD), c2));
+                const float wb = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(rR, rij), rD), c2));
+                const float wg = __builtin_amdgcn_exp2f(__fmul_rn(__fsub_rn(__fsub_rn(gR, rij), gD), c2));
+                buf[u * WAVE] = make_float4(wa, wb, wg, 0.0f);
+            }
             const float mR = act ? rij : NINF;
             const float mD = act ? d : 0.0f;
             rR = mR;
@@ -2353,12 +2382,12 @@ bwd_kernel(DPParams P) {
     static_assert(GW == 0 || KXOf<Cost>::value > 0, "gradient mode needs matrix-core cost tiles");
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ __align__(16) double tab[kTabBytesBwd / 8];
-    // with weight waves (P.ww: costs from D, hardware exp2, W = 1; waves compute 0,
-    // producer 1, helper 2, weights 3 and 5, 4 idle, so that each weight wave shares its
-    // SIMD with a light wave) their stage follows the handoff rings
-    constexpr bool WW_OK = std::is_same<Cost, CostD>::value && !EXACT && GW == 0;
+    // with weight waves (P.ww: costs from D, W = 1; waves compute 0, producer 1, helper 2,
+    // weights 3 and 5, 4 idle, so that each weight wave shares its SIMD with a light wave)
+    // their stage (P.ww planes) follows the handoff rings
+    constexpr bool WW_OK = std::is_same<Cost, CostD>::value && GW == 0;
     const bool ww = WW_OK && P.ww;
-    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W) + (ww ? kWStageBytes : 0), kTabBytesBwd, tab};
+    Smem sm{smem_raw, P.W, ring_bytes_bwd(P.W) + (ww ? P.ww * kWStageBytes : 0), kTabBytesBwd, tab};
     // wave-uniform values are moved to scalar registers so that the branches on band,
     // group and pair compile to scalar branches, not exec-masked regions
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -2398,13 +2427,13 @@ bwd_kernel(DPParams P) {
         if constexpr (WW_OK) {
             if (ww) {  // one band per workgroup (g is the band)
                 if (w == 3 || w == 5) {
-                    bwd_weight_wave(P, sm, p, g, w == 3 ? 0 : 1);
+                    bwd_weight_wave<EXACT>(P, sm, p, g, w == 3 ? 0 : 1);
                 } else if (w == 1) {
                     producer_wave<Cost, true>(P, sm, p, g, 0);
                 } else if (w == 0) {
                     CostRing cost;
                     cost.bind(sm, 0, P);
-                    bwd_band<CostRing, BAND, false, true>(P, cost, sm, p, g, 0);
+                    bwd_band<CostRing, BAND, EXACT, true>(P, cost, sm, p, g, 0);
                 }
                 return;
             }
@@ -2433,7 +2462,7 @@ bwd_kernel(DPParams P) {
 hipError_t launch_dp_prep(const DPParams& P, bool bwd, hipStream_t st);
 
 inline size_t dp_smem_bytes(const DPParams& P, bool bwd) {
-    const size_t ring = bwd ? ring_bytes_bwd(P.W) + (P.ww ? kWStageBytes : 0)
+    const size_t ring = bwd ? ring_bytes_bwd(P.W) + P.ww * kWStageBytes
                             : ring_bytes_fwd(P.W) + (P.lin ? lin_extra_bytes(P.W) : 0);
     return 256 + ring + (size_t)P.W * WAVE * CS * sizeof(float);  // the tables are static
 }
@@ -2463,9 +2492,11 @@ hipError_t launch_dp(K kernel, const DPParams& P, bool bwd, bool produced, hipSt
 template <class Cost, bool BWD, bool EXACT>
 hipError_t launch_cost(const DPParams& P, hipStream_t st) {
     if constexpr (BWD) {
-        // the weight wave only where the kernel has it (costs from D, hardware exp2, W = 1)
+        // weight waves only where the kernel has them (costs from D, W = 1); their stage
+        // has one plane under hardware exp2, two under exact arithmetic (double weights)
         DPParams Q = P;
-        if (!std::is_same<Cost, CostD>::value || EXACT || P.W != 1) Q.ww = 0;
+        if (!std::is_same<Cost, CostD>::value || P.W != 1) Q.ww = 0;
+        else if (Q.ww) Q.ww = EXACT ? 2 : 1;
         if (Q.bw > 0.0) return launch_dp(bwd_kernel<Cost, true, EXACT>, Q, true, Produced<Cost, true>::value, st);
         return launch_dp(bwd_kernel<Cost, false, EXACT>, Q, true, Produced<Cost, true>::value, st);
     } else {

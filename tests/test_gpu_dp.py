@@ -232,7 +232,7 @@ def test_fused_matches_unfused_kernels(mode):
             torch.testing.assert_close(o2.cpu(), out_o, rtol=FWD_RTOL, atol=0)
 
 
-@pytest.mark.parametrize("mode", ["mixed", "fast"])
+@pytest.mark.parametrize("mode", ["mixed", "fast", "exact"])
 @pytest.mark.parametrize("B,N,M,gamma,bw", [
     (4, 512, 512, 1.0, -1.0),    # full bands, the row below read from the next band's R and D
     (3, 150, 120, 0.7, 30.0),    # Sakoe-Chiba band, a partial last band
@@ -240,9 +240,9 @@ def test_fused_matches_unfused_kernels(mode):
     (3, 70, 10, 1.0, -1.0),      # fewer columns than a group
 ])
 def test_weight_wave_backward_matches_classic(mode, B, N, M, gamma, bw):
-    # The D-reading backward under hardware exp2 takes one band per workgroup with a weight
-    # wave where the batch's one-band workgroups all fit on the GPU, else the classic
-    # geometry (4 bands per workgroup, the weights in the compute wave).  Pairs are
+    # The D-reading backward takes one band per workgroup with weight waves where the
+    # batch's one-band workgroups all fit on the GPU, else the classic geometry (4 bands per
+    # workgroup, the weights in the compute wave).  Pairs are
     # independent, so the same pairs inside a batch too large for one-band workgroups give
     # the classic result: G must be identical to the bit, with an upstream gradient too.
     nb = (N + 63) // 64
