@@ -41,9 +41,10 @@ struct DPParams {
     int lin;            // forward under mixed arithmetic, matrix-core costs, no band, W <= 2:
                         // pairs whose costs allow it run the scaled linear-domain recursion
                         // (fwd_band_lin)
-    int ww;             // backward with costs read from D, hardware exp2 (mixed or fast
-                        // arithmetic), W == 1: a weight wave per band forms each cell's three
-                        // weights ahead of the compute wave (bwd_weight_wave)
+    int ww;             // backward with costs read from D, W == 1: two weight waves per band
+                        // form each cell's three weights ahead of the compute wave
+                        // (bwd_weight_wave); 1 under hardware exp2, 2 under exact arithmetic
+                        // (the stage's planes, set by the launch)
     int nb, W, G;       // 64-row bands per pair, waves per workgroup, workgroups per pair
     int S;              // steps per band in the R table (dp_band_steps(M))
     double gamma, inv_gamma, bw;
