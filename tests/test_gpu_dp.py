@@ -264,6 +264,38 @@ def test_weight_wave_backward_matches_classic(mode, B, N, M, gamma, bw):
     assert torch.equal(Gs, Gbig[:B])
 
 
+@pytest.mark.parametrize("mode", ["mixed", "exact"])
+def test_weight_wave_backward_nonfinite_costs(mode):
+    # +inf costs (pair 0, two of them on the rows either side of a band boundary; +inf R
+    # maps to -inf, so some cells' weights are exp(+inf) and their E is NaN, as in the
+    # reference's kernels) and a NaN cost (pair 1; the reference's kernels take any D): the
+    # weight-wave geometry gives the classic geometry's G to the bit where it is a number,
+    # and NaN in the same cells (the sign of a NaN result is not specified, and the
+    # compilers' forms of a - b differ in it).
+    B, N, M = 2, 130, 90
+    nb = (N + 63) // 64
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    Bbig = cus // nb + 1
+    say(f"[weight wave, non-finite D] mode={mode} B={B} (classic batch {Bbig}) N={N} M={M}")
+    g = torch.Generator().manual_seed(7)
+    D = torch.rand((Bbig, N, M), generator=g) * 3.0
+    D[0, 5, 7] = float("inf")
+    D[0, 64, 40] = float("inf")       # the first row of a band below
+    D[0, 63, 41] = float("inf")       # the last row of a band above
+    D[1, 100, 3] = float("nan")
+    D = D.cuda()
+    with numerics(mode):
+        _, R = _engine.dtw_fwd(D, 0.8, -1.0)
+        Gbig = _engine.dtw_bwd(D, R, 0.8, -1.0)
+        S = (M + 63 + 15) // 16 * 16
+        Gs = _engine.dtw_bwd(D[:B].contiguous(), R[:B * nb * S * 64].contiguous(), 0.8, -1.0)
+    Gc = Gbig[:B]
+    nan_s, nan_c = torch.isnan(Gs), torch.isnan(Gc)
+    assert nan_s[1].any() and (~nan_s[0]).any()
+    assert torch.equal(nan_s, nan_c)
+    assert torch.equal(Gs[~nan_s].view(torch.int32), Gc[~nan_c].view(torch.int32))
+
+
 @pytest.mark.parametrize("B,N,M,K,gamma,scale", [
     (32, 512, 512, 64, 1.0, None),   # the headline shape: one band per workgroup
     (64, 512, 128, 16, 0.5, None),   # 512 bands: two per workgroup (LDS and global handover)
