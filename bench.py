@@ -388,8 +388,9 @@ def main(argv=None):
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this engine is measured on one GPU only (pairs shard across GPUs "
-              "with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this engine is measured on one GPU only (pairs are independent, so "
+              "a batch shards across GPUs by pairs with no exchange). Run with --gpus 1.",
+              file=sys.stderr)
         return 2
 
     import torch
